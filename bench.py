@@ -1,0 +1,354 @@
+#!/usr/bin/env python3
+"""Benchmark of the grxBLAS / grxDNN hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only NAME]
+
+Prints ONE JSON line. The headline `value` is BASELINE config 2: bf16
+grxblasGemmEx at M=N=K=8192 (row-major A x column-major B, i.e. transa=T,
+transb=N; fp32 accumulate, bf16 C), in TFLOP/s of algorithmic work
+2*M*N*K per launch. A "step" is one GemmEx call over resident HBM inputs.
+The other BASELINE configs (bf16 4096^3, int8 GEMM + per-channel dequant,
+RMSNorm / LayerNorm, causal attention) are reported under "ops", each with its
+own roofline. Every kernel time is the HIP-event time of K back-to-back
+launches on the library handle's stream divided by K.
+
+The CPU baseline (rank 0, N=1) times the oracle -- the reference's own CPU
+GEMM loop restated in C (ref tests/libs/test_grxblas_ex.cpp:45-63) -- on a
+bounded slice of the same workload on the host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import grxcp_amd as g  # noqa: E402
+from grxcp_amd import synth  # noqa: E402
+
+PEAK = {"bf16": 2500.0, "int8": 5000.0, "hbm": 8000.0}  # TFLOP/s, TOP/s, GB/s (MI355X dense)
+BF16, I8, I32 = g.GRX_R_16BF, g.GRX_R_8I, g.GRX_R_32I
+
+
+def log(msg: str) -> None:
+    sys.stderr.write(f"[bench] {msg}\n")
+    sys.stderr.flush()
+
+
+def time_launches(stream: g.Stream, launch, steps: int, warmup: int) -> float:
+    """Mean milliseconds per launch over `steps` launches (after `warmup`),
+    measured with HIP events on the launching stream."""
+    for _ in range(warmup):
+        launch()
+    g.synchronize()
+    e0, e1 = g.Event(), g.Event()
+    e0.record(stream.s)
+    for _ in range(steps):
+        launch()
+    e1.record(stream.s)
+    ms = e0.elapsed_ms(e1)
+    g.synchronize()
+    e0.close()
+    e1.close()
+    return ms / steps
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE),
+    as committed under profiles/ by the profiling runs; None if not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        return json.load(open(path)).get(name, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def roofline(bound: str, work: float, ms: float, peak_key: str, traffic_key: str):
+    if bound == "hbm":
+        achieved = work / (ms * 1e-3) / 1e9      # GB/s
+        unit = "GB/s"
+    else:
+        achieved = work / (ms * 1e-3) / 1e12     # TFLOP/s (TOP/s for int8)
+        unit = "TFLOP/s" if peak_key == "bf16" else "TOP/s"
+    peak = PEAK[peak_key]
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(traffic_key)}
+
+
+# ---- CPU baseline -------------------------------------------------------------
+
+def cpu_threads() -> int:
+    n = os.cpu_count() or 1
+    cap = int(os.environ.get("OMP_NUM_THREADS", n))
+    return max(1, min(n, cap))
+
+
+def cpu_gemm_baseline(A_bits, B_bits, M, N, K, target_s=10.0):
+    """Oracle fp32-accumulate GemmEx loop on whole rows of M, slice by slice,
+    until ~target_s of CPU time; returns TFLOP/s and the sample description."""
+    import oracle as O
+    threads = cpu_threads()
+    O.set_threads(threads)
+    Bf = O.bf16_to_f32(B_bits)                      # column-major K x N
+    done, spent, rows_per = 0, 0.0, 16
+    while spent < target_s and done < M:
+        r = min(rows_per, M - done)
+        a = O.bf16_to_f32(A_bits[done * K:(done + r) * K])
+        t0 = time.perf_counter()
+        O.gemm_f32acc(1, 0, r, N, K, 1.0, a, K, Bf, K, 0.0, np.zeros(r * N, np.float32), r)
+        spent += time.perf_counter() - t0
+        done += r
+    flops = 2.0 * done * N * K
+    return {"value": round(flops / spent / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{done} of {M} rows of M ({flops / 1e9:.1f} GFLOP) through the oracle's "
+                      f"fp32-accumulate GemmEx loop, {threads} OpenMP threads, {spent:.1f} s"}
+
+
+def cpu_igemm_baseline(A, B, M, N, K, target_s=5.0):
+    import oracle as O
+    threads = cpu_threads()
+    O.set_threads(threads)
+    done, spent = 0, 0.0
+    while spent < target_s and done < M:
+        r = min(16, M - done)
+        t0 = time.perf_counter()
+        O.igemm(1, 0, r, N, K, 1, A[done * K:(done + r) * K], K, B, K, 0, np.zeros(r * N, np.int32), r)
+        spent += time.perf_counter() - t0
+        done += r
+    ops = 2.0 * done * N * K
+    return {"value": round(ops / spent / 1e12, 6), "unit": "TOP/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of {M} rows ({ops / 1e9:.1f} GOP), oracle int32 GEMM, {threads} threads"}
+
+
+def cpu_norm_baseline(x_bits, gamma_bits, beta_bits, rows, hidden, layer):
+    import oracle as O
+    threads = cpu_threads()
+    O.set_threads(threads)
+    r = min(rows, 2048)
+    x = O.bf16_to_f32(x_bits[: r * hidden]).reshape(r, hidden)
+    gf, bf = O.bf16_to_f32(gamma_bits), O.bf16_to_f32(beta_bits)
+    t0 = time.perf_counter()
+    if layer:
+        O.layernorm(x, gf, bf, 1e-6)
+    else:
+        O.rmsnorm(x, gf, 1e-6)
+    dt = time.perf_counter() - t0
+    moved = r * hidden * 4 + hidden * 2 * (2 if layer else 1)   # bf16 in + bf16 out
+    return {"value": round(moved / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{r} of {rows} rows, oracle fp64 norm, {threads} threads"}
+
+
+def cpu_attention_baseline(q, k, v, S, D, rows=256):
+    import oracle as O
+    threads = cpu_threads()
+    O.set_threads(threads)
+    t0 = time.perf_counter()
+    r0 = S - rows
+    O.attention_head(q, k, v, True, D ** -0.5, r0, S)
+    dt = time.perf_counter() - t0
+    flops = sum(4.0 * D * (i + 1) for i in range(r0, S))
+    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"one (b,h), last {rows} query rows ({flops / 1e9:.2f} GFLOP), oracle fp64, "
+                      f"{threads} threads"}
+
+
+# ---- GPU workloads --------------------------------------------------------------
+
+def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu):
+    N = K = M
+    log(f"bf16 GemmEx {M}^3: generating inputs")
+    A = synth.normal_bf16(M * K, 21)
+    B = synth.normal_bf16(N * K, 22)
+    dA, dB, dC = g.DeviceBuffer.from_array(A), g.DeviceBuffer.from_array(B), g.DeviceBuffer(M * N * 2)
+    one, zero = g.fptr(1.0), g.fptr(0.0)
+
+    def launch():
+        s = blas.L.grxblasGemmEx(blas.h, 1, 0, M, N, K, one, dA.p, BF16, K, dB.p, BF16, K, zero, dC.p,
+                                 BF16, M)
+        if s:
+            raise g.GrxError(f"GemmEx status {s}")
+    log(f"bf16 GemmEx {M}^3: timing")
+    ms = time_launches(stream, launch, steps, warmup)
+    flops = 2.0 * M * N * K
+    out = {"name": f"gemm_bf16_{M}", "ms": round(ms, 4), "value": round(flops / ms / 1e9, 2),
+           "unit": "TFLOP/s", "roofline": roofline("mfma", flops, ms, "bf16", f"gemm_bf16_{M}")}
+    if cpu:
+        log("bf16 GemmEx: CPU baseline")
+        out["cpu_baseline"] = cpu_gemm_baseline(A, B, M, N, K)
+    for d in (dA, dB, dC):
+        d.close()
+    return out
+
+
+def bench_gemm_int8(stream, blas, steps, warmup, cpu):
+    M, K, N = 4096, 8192, 28672
+    log("int8 GEMM + dequant: generating inputs")
+    A = synth.uniform_int8(M * K, 31)
+    B = synth.uniform_int8(N * K, 32)
+    scale = synth.uniform_f32(N, 33, 0.001, 0.01)
+    dA, dB = g.DeviceBuffer.from_array(A), g.DeviceBuffer.from_array(B)
+    dS, dY = g.DeviceBuffer.from_array(scale), g.DeviceBuffer(M * N * 2)
+
+    def launch():
+        s = blas.L.grxblasGemmExDequant(blas.h, 1, 0, M, N, K, dA.p, I8, K, dB.p, I8, K, dS.p, dY.p,
+                                        BF16, M)
+        if s:
+            raise g.GrxError(f"GemmExDequant status {s}")
+    log("int8 GEMM + dequant: timing")
+    ms = time_launches(stream, launch, steps, warmup)
+    ops = 2.0 * M * N * K
+    out = {"name": "gemm_int8_dequant_4096x28672x8192", "ms": round(ms, 4),
+           "value": round(ops / ms / 1e9, 2), "unit": "TOP/s",
+           "roofline": roofline("mfma", ops, ms, "int8", "gemm_int8_dequant")}
+    if cpu:
+        log("int8: CPU baseline")
+        out["cpu_baseline"] = cpu_igemm_baseline(A, B, M, N, K)
+    for d in (dA, dB, dS, dY):
+        d.close()
+    return out
+
+
+def bench_norm(stream, dnn, layer, steps, warmup, cpu):
+    rows, hidden = 16384, 8192
+    name = "layernorm" if layer else "rmsnorm"
+    log(f"{name}: generating inputs")
+    xs = [synth.normal_bf16(rows * hidden, 41 + i) for i in range(2)]
+    gb = synth.normal_bf16(hidden, 43, 1.0, 0.02)
+    bb = synth.normal_bf16(hidden, 44, 0.0, 0.02)
+    # two buffer sets, alternated, so reads stream from HBM rather than the
+    # 256 MB Infinity Cache
+    dx = [g.DeviceBuffer.from_array(x) for x in xs]
+    dy = [g.DeviceBuffer(rows * hidden * 2) for _ in range(2)]
+    dg, db = g.DeviceBuffer.from_array(gb), g.DeviceBuffer.from_array(bb)
+    xd, wd = g.TensorDesc(BF16, [rows, hidden]), g.TensorDesc(BF16, [hidden])
+    state = {"i": 0}
+
+    def launch():
+        i = state["i"] & 1
+        state["i"] += 1
+        s = (dnn.layernorm(xd, dx[i].p, wd, dg.p, db.p, 1e-6, xd, dy[i].p) if layer
+             else dnn.rmsnorm(xd, dx[i].p, wd, dg.p, 1e-6, xd, dy[i].p))
+        if s:
+            raise g.GrxError(f"{name} status {s}")
+    log(f"{name}: timing")
+    ms = time_launches(stream, launch, steps, warmup)
+    moved = rows * hidden * 2 * 2 + hidden * 2 * (2 if layer else 1)
+    out = {"name": f"{name}_16384x8192", "ms": round(ms, 5), "value": round(moved / ms / 1e6, 1),
+           "unit": "GB/s", "roofline": roofline("hbm", moved, ms, "hbm", name)}
+    if cpu:
+        out["cpu_baseline"] = cpu_norm_baseline(xs[0], gb, bb, rows, hidden, layer)
+    for d in dx + dy + [dg, db]:
+        d.close()
+    return out
+
+
+def bench_attention(stream, dnn, steps, warmup, cpu):
+    B, H, S, D = 4, 32, 4096, 128
+    n = B * H * S * D
+    log("attention: generating inputs")
+    qb, kb, vb = (synth.normal_bf16(n, s) for s in (51, 52, 53))
+    dq, dk, dv = (g.DeviceBuffer.from_array(a) for a in (qb, kb, vb))
+    do = g.DeviceBuffer(n * 2)
+    desc = g.TensorDesc(BF16, [B, H, S, D])
+    ad = g.AttnDesc(True, D ** -0.5)
+
+    def launch():
+        s = dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p)
+        if s:
+            raise g.GrxError(f"attention status {s}")
+    log("attention: timing")
+    ms = time_launches(stream, launch, steps, warmup)
+    flops = 4.0 * D * B * H * S * (S + 1) / 2
+    out = {"name": "attention_causal_b4h32s4096d128", "ms": round(ms, 4),
+           "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
+           "roofline": roofline("mfma", flops, ms, "bf16", "attention")}
+    if cpu:
+        import oracle as O
+        q = O.bf16_to_f32(qb[: S * D]).reshape(S, D)
+        k = O.bf16_to_f32(kb[: S * D]).reshape(S, D)
+        v = O.bf16_to_f32(vb[: S * D]).reshape(S, D)
+        out["cpu_baseline"] = cpu_attention_baseline(q, k, v, S, D)
+    for d in (dq, dk, dv, do):
+        d.close()
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}).",
+              file=sys.stderr)
+        return 2
+    only = set(filter(None, args.only.split(",")))
+    want = lambda n: not only or n in only  # noqa: E731
+    cpu = not args.no_cpu_baseline
+
+    g.load()
+    g.check_rt(g.load().rt.grxSetDevice(0), "grxSetDevice")
+    stream = g.Stream()
+    blas, dnn = g.Blas(), g.Dnn()
+    blas.set_stream(stream.s)
+    dnn.set_stream(stream.s)
+
+    headline = None
+    ops = []
+    if want("gemm"):
+        headline = bench_gemm_bf16(stream, blas, 8192, args.steps, args.warmup, cpu)
+    if want("gemm4096"):
+        ops.append(bench_gemm_bf16(stream, blas, 4096, args.steps, args.warmup, False))
+    if want("int8"):
+        ops.append(bench_gemm_int8(stream, blas, args.steps, args.warmup, cpu))
+    if want("rmsnorm"):
+        ops.append(bench_norm(stream, dnn, False, args.steps, args.warmup, cpu))
+    if want("layernorm"):
+        ops.append(bench_norm(stream, dnn, True, args.steps, args.warmup, cpu))
+    if want("attention"):
+        ops.append(bench_attention(stream, dnn, args.steps, args.warmup, cpu))
+
+    if headline is None:
+        headline = ops.pop(0)
+    line = {
+        "metric": "GEMM/attention TFLOP/s (bf16, int8), RMSNorm GB/s; % of MI355X peak",
+        "value": headline["value"],
+        "unit": headline["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": headline["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) bf16 (PCG64), resident in HBM before timing",
+        "config": {"workload": "grxblasGemmEx bf16 M=N=K=8192, transa=T transb=N (row-major A x "
+                               "column-major B), fp32 accumulate, bf16 C, alpha=1 beta=0",
+                   "m": 8192, "n": 8192, "k": 8192},
+        "roofline": headline["roofline"],
+        "cpu_baseline": headline.get("cpu_baseline"),
+        "ops": ops,
+    }
+    print(json.dumps(line))
+    sys.stdout.flush()
+    blas.close()
+    dnn.close()
+    stream.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

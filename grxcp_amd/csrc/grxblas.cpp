@@ -1,0 +1,464 @@
+// libgrxblas.so -- grxBLAS host library for gfx950.
+//
+// Keeps the reference's API contract (ref: src/libs/grxblas/grxblas.cpp):
+// the same validation order and status codes, calls asynchronous on the
+// handle's stream, no silent fallback for an unsupported type pairing. What
+// changes is everything under it: there is no .vxbin module to load, no
+// shape-query kernel and no DXA descriptor to program -- the gfx950 kernels
+// are compiled into this library and launched directly on the HIP stream.
+
+#include <grx/grxblas.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include <dlfcn.h>
+#include <limits.h>
+#include <stdlib.h>
+
+#include <array>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+
+#include "hip_status.h"
+#include "launch.h"
+
+struct grxblasContext {
+  hipStream_t stream = nullptr;
+  std::mutex mutex;
+  std::string kernel_path;           // set by the first successful kernel lookup
+  std::array<signed char, 64> device_ok{};  // per device: 0 unknown, 1 ok, -1 refused
+  grxblasStatus_t device_status[64];
+  grxCycleSlot* probe = nullptr;
+  int probe_capacity = 0;
+  int slot_a = 0, slot_b = 1;
+};
+
+namespace {
+
+std::mutex g_path_mutex;
+std::string g_kernel_path;
+
+// This library's own file: the kernels live in it.
+std::string self_path() {
+  Dl_info info{};
+  if (dladdr((void*)&grxblasCreate, &info) == 0 || !info.dli_fname) return {};
+  char buf[PATH_MAX];
+  if (!realpath(info.dli_fname, buf)) return info.dli_fname;
+  return buf;
+}
+
+// Configured source first, with no fallback past it (the reference's rule,
+// ref src/libs/grxblas/grxblas.cpp:33-58): a configured directory that is not
+// the one holding this library's kernels is an error, not a hint.
+grxblasStatus_t ensure_kernels_locked(grxblasContext& ctx) {
+  if (!ctx.kernel_path.empty()) return GRXBLAS_STATUS_SUCCESS;
+  std::string configured;
+  {
+    std::lock_guard<std::mutex> lock(g_path_mutex);
+    configured = g_kernel_path;
+  }
+  if (configured.empty()) {
+    const char* env = std::getenv("GRXBLAS_KERNEL_PATH");
+    if (env) configured = env;
+  }
+  const std::string self = self_path();
+  if (!configured.empty()) {
+    const std::string want = configured + "/libgrxblas.so";
+    char buf[PATH_MAX];
+    const bool same = realpath(want.c_str(), buf) && self == buf;
+    if (!same) {
+      std::fprintf(stderr,
+                   "grxblas: the gfx950 kernels are in %s, not in the configured "
+                   "directory %s.\n"
+                   "         Point GRXBLAS_KERNEL_PATH / grxblasSetKernelPath at the "
+                   "directory holding libgrxblas.so, or unset it.\n",
+                   self.c_str(), configured.c_str());
+      return GRXBLAS_STATUS_NOT_INITIALIZED;
+    }
+  }
+  ctx.kernel_path = self;
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+// The device must be a gfx950: the library carries gfx950 code objects only.
+grxblasStatus_t ensure_device_locked(grxblasContext& ctx) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    static bool said = false;
+    if (!said) {
+      said = true;
+      std::fprintf(stderr, "grxblas: no HIP device is available.\n");
+    }
+    return GRXBLAS_STATUS_ARCH_MISMATCH;
+  }
+  if (dev >= (int)ctx.device_ok.size()) return GRXBLAS_STATUS_NOT_SUPPORTED;
+  if (ctx.device_ok[dev] == 1) return GRXBLAS_STATUS_SUCCESS;
+  if (ctx.device_ok[dev] == -1) return ctx.device_status[dev];
+  hipDeviceProp_t p;
+  grxblasStatus_t st = GRXBLAS_STATUS_SUCCESS;
+  if (hipGetDeviceProperties(&p, dev) != hipSuccess) {
+    st = GRXBLAS_STATUS_INTERNAL_ERROR;
+  } else if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0 || p.warpSize != 64) {
+    std::fprintf(stderr,
+                 "grxblas: this build carries gfx950 kernels (wave64); device %d is %s "
+                 "(warp %d).\n",
+                 dev, p.gcnArchName, p.warpSize);
+    st = GRXBLAS_STATUS_ARCH_MISMATCH;
+  }
+  ctx.device_ok[dev] = (st == GRXBLAS_STATUS_SUCCESS) ? 1 : -1;
+  ctx.device_status[dev] = st;
+  return st;
+}
+
+grxblasStatus_t ensure_ready(grxblasContext& ctx) {
+  std::lock_guard<std::mutex> lock(ctx.mutex);
+  grxblasStatus_t s = ensure_kernels_locked(ctx);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+  return ensure_device_locked(ctx);
+}
+
+// HIP errors to grxBLAS status (the role of ref grxblas.cpp:173-182).
+grxblasStatus_t from_hip(hipError_t e) {
+  switch (grx_from_hip(e)) {
+    case grxSuccess:                   return GRXBLAS_STATUS_SUCCESS;
+    case grxErrorMemoryAllocation:     return GRXBLAS_STATUS_ALLOC_FAILED;
+    case grxErrorInvalidValue:         return GRXBLAS_STATUS_INVALID_VALUE;
+    case grxErrorInvalidDevicePointer: return GRXBLAS_STATUS_INVALID_VALUE;
+    case grxErrorNotSupported:         return GRXBLAS_STATUS_NOT_SUPPORTED;
+    case grxErrorInvalidKernelImage:   return GRXBLAS_STATUS_ARCH_MISMATCH;
+    default:                           return GRXBLAS_STATUS_EXECUTION_FAILED;
+  }
+}
+
+bool integral(float v) {
+  return std::isfinite(v) && v >= -2147483648.0f && v < 2147483648.0f &&
+         v == (float)(int32_t)v;
+}
+
+constexpr unsigned kTypeMask = GRXBLAS_TENSOR_FP16 | GRXBLAS_TENSOR_BF16 | GRXBLAS_TENSOR_INT8;
+
+void say_types_once() {
+  static bool said = false;
+  if (said) return;
+  said = true;
+  std::fprintf(stderr,
+               "grxblas: grxblasGemmEx accepts (16F,16F,32F), (16F,16F,16F), (16BF,16BF,32F), "
+               "(16BF,16BF,16BF)\n         and (8I,8I,32I); int8 to bf16 with a per-column "
+               "scale is grxblasGemmExDequant.\n");
+}
+
+// Probe slots for a launch: checked against the attached capacity.
+grxblasStatus_t probe_for(grxblasContext& ctx, int64_t needed, grxCycleSlot** out) {
+  std::lock_guard<std::mutex> lock(ctx.mutex);
+  *out = nullptr;
+  if (!ctx.probe) return GRXBLAS_STATUS_SUCCESS;
+  if ((int64_t)ctx.probe_capacity < needed) return GRXBLAS_STATUS_INVALID_VALUE;
+  *out = ctx.probe;
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* grxblasGetStatusString(grxblasStatus_t s) {
+  switch (s) {
+    case GRXBLAS_STATUS_SUCCESS:          return "success";
+    case GRXBLAS_STATUS_NOT_INITIALIZED:  return "library not initialized (kernels not found?)";
+    case GRXBLAS_STATUS_ALLOC_FAILED:     return "allocation failed";
+    case GRXBLAS_STATUS_INVALID_VALUE:    return "invalid argument";
+    case GRXBLAS_STATUS_ARCH_MISMATCH:    return "device lacks a required capability";
+    case GRXBLAS_STATUS_EXECUTION_FAILED: return "kernel execution failed";
+    case GRXBLAS_STATUS_NOT_SUPPORTED:    return "not supported";
+    case GRXBLAS_STATUS_INTERNAL_ERROR:   return "internal error";
+  }
+  return "unknown status";
+}
+
+grxblasStatus_t grxblasCreate(grxblasHandle_t* handle) {
+  if (!handle) return GRXBLAS_STATUS_INVALID_VALUE;
+  *handle = new (std::nothrow) grxblasContext();
+  return *handle ? GRXBLAS_STATUS_SUCCESS : GRXBLAS_STATUS_ALLOC_FAILED;
+}
+
+grxblasStatus_t grxblasDestroy(grxblasHandle_t handle) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  delete handle;
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+grxblasStatus_t grxblasSetStream(grxblasHandle_t handle, grxStream_t stream) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  handle->stream = reinterpret_cast<hipStream_t>(stream);
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+grxblasStatus_t grxblasGetStream(grxblasHandle_t handle, grxStream_t* stream) {
+  if (!handle || !stream) return GRXBLAS_STATUS_INVALID_VALUE;
+  *stream = reinterpret_cast<grxStream_t>(handle->stream);
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+grxblasStatus_t grxblasSetKernelPath(const char* path) {
+  std::lock_guard<std::mutex> lock(g_path_mutex);
+  g_kernel_path = path ? path : "";
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+grxblasStatus_t grxblasSetTensorMapSlots(grxblasHandle_t handle, int slotA, int slotB) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (slotA < 0 || slotB < 0 || slotA == slotB) return GRXBLAS_STATUS_INVALID_VALUE;
+  std::lock_guard<std::mutex> lock(handle->mutex);
+  handle->slot_a = slotA;
+  handle->slot_b = slotB;
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+grxblasStatus_t grxblasGetTensorTypes(grxblasHandle_t handle, unsigned* typeMask) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!typeMask) return GRXBLAS_STATUS_INVALID_VALUE;
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+  *typeMask = kTypeMask;
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+grxblasStatus_t grxblasGetTensorTile(grxblasHandle_t handle, int* m, int* n, int* k) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!m || !n || !k) return GRXBLAS_STATUS_INVALID_VALUE;
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+  *m = 32;
+  *n = 32;
+  *k = 16;
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+grxblasStatus_t grxblasGemmEx(grxblasHandle_t handle, grxblasOperation_t transa,
+                              grxblasOperation_t transb, int m, int n, int k,
+                              const float* alpha, const void* A, grxDataType_t Atype, int lda,
+                              const void* B, grxDataType_t Btype, int ldb, const float* beta,
+                              void* C, grxDataType_t Ctype, int ldc) {
+  // Validation order of ref src/libs/grxblas/grxblas.cpp:507-524.
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!alpha || !beta) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m < 0 || n < 0 || k < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m == 0 || n == 0) return GRXBLAS_STATUS_SUCCESS;
+  if (k > 0 && (!A || !B)) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (!C) return GRXBLAS_STATUS_INVALID_VALUE;
+  const bool ta = (transa == GRXBLAS_OP_T);
+  const bool tb = (transb == GRXBLAS_OP_T);
+  if (lda < (ta ? k : m) || ldb < (tb ? n : k) || ldc < m) return GRXBLAS_STATUS_INVALID_VALUE;
+
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+
+  // Type pairing after the device is known (ref grxblas.cpp:552-575).
+  grxk::MmaIn in;
+  grxk::MmaOut out;
+  if (Atype == GRX_R_16F && Btype == GRX_R_16F && Ctype == GRX_R_32F) {
+    in = grxk::MmaIn::F16; out = grxk::MmaOut::F32;
+  } else if (Atype == GRX_R_16F && Btype == GRX_R_16F && Ctype == GRX_R_16F) {
+    in = grxk::MmaIn::F16; out = grxk::MmaOut::F16;
+  } else if (Atype == GRX_R_16BF && Btype == GRX_R_16BF && Ctype == GRX_R_32F) {
+    in = grxk::MmaIn::BF16; out = grxk::MmaOut::F32;
+  } else if (Atype == GRX_R_16BF && Btype == GRX_R_16BF && Ctype == GRX_R_16BF) {
+    in = grxk::MmaIn::BF16; out = grxk::MmaOut::BF16;
+  } else if (Atype == GRX_R_8I && Btype == GRX_R_8I && Ctype == GRX_R_32I) {
+    in = grxk::MmaIn::I8; out = grxk::MmaOut::I32;
+  } else {
+    say_types_once();
+    return GRXBLAS_STATUS_NOT_SUPPORTED;
+  }
+  // Integral alpha/beta for the int8 pairing (ref grxblas.cpp:577-584).
+  if (in == grxk::MmaIn::I8 && (!integral(*alpha) || !integral(*beta)))
+    return GRXBLAS_STATUS_INVALID_VALUE;
+
+  grxCycleSlot* probe = nullptr;
+  const grxblasStatus_t ps = probe_for(*handle, grxk::gemm_probe_slots(m, n), &probe);
+  if (ps != GRXBLAS_STATUS_SUCCESS) return ps;
+
+  grxk::GemmDesc d{};
+  d.m = m; d.n = n; d.k = k;
+  d.ta = ta; d.tb = tb;
+  d.a = A; d.lda = lda;
+  d.b = B; d.ldb = ldb;
+  d.c = C; d.ldc = ldc;
+  d.alpha = *alpha; d.beta = *beta;
+  if (in == grxk::MmaIn::I8) { d.ialpha = (int32_t)*alpha; d.ibeta = (int32_t)*beta; }
+  d.probe = probe;
+  return from_hip(grxk::launch_mma_gemm(in, out, d, handle->stream));
+}
+
+grxblasStatus_t grxblasGemmExDequant(grxblasHandle_t handle, grxblasOperation_t transa,
+                                     grxblasOperation_t transb, int m, int n, int k,
+                                     const void* A, grxDataType_t Atype, int lda,
+                                     const void* B, grxDataType_t Btype, int ldb,
+                                     const float* scaleN, void* C, grxDataType_t Ctype,
+                                     int ldc) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (m < 0 || n < 0 || k < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m == 0 || n == 0) return GRXBLAS_STATUS_SUCCESS;
+  if (k > 0 && (!A || !B)) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (!C || !scaleN) return GRXBLAS_STATUS_INVALID_VALUE;
+  const bool ta = (transa == GRXBLAS_OP_T);
+  const bool tb = (transb == GRXBLAS_OP_T);
+  if (lda < (ta ? k : m) || ldb < (tb ? n : k) || ldc < m) return GRXBLAS_STATUS_INVALID_VALUE;
+
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+  if (!(Atype == GRX_R_8I && Btype == GRX_R_8I && Ctype == GRX_R_16BF)) {
+    static bool said = false;
+    if (!said) {
+      said = true;
+      std::fprintf(stderr, "grxblas: grxblasGemmExDequant takes (8I, 8I, 16BF) only.\n");
+    }
+    return GRXBLAS_STATUS_NOT_SUPPORTED;
+  }
+  grxCycleSlot* probe = nullptr;
+  const grxblasStatus_t ps = probe_for(*handle, grxk::gemm_probe_slots(m, n), &probe);
+  if (ps != GRXBLAS_STATUS_SUCCESS) return ps;
+
+  grxk::GemmDesc d{};
+  d.m = m; d.n = n; d.k = k;
+  d.ta = ta; d.tb = tb;
+  d.a = A; d.lda = lda;
+  d.b = B; d.ldb = ldb;
+  d.c = C; d.ldc = ldc;
+  d.scale = scaleN;
+  d.probe = probe;
+  return from_hip(grxk::launch_mma_gemm(grxk::MmaIn::I8, grxk::MmaOut::DEQ_BF16, d,
+                                        handle->stream));
+}
+
+grxblasStatus_t grxblasSetCycleProbe(grxblasHandle_t handle, grxCycleSlot* slots, int capacity) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (slots && capacity <= 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  std::lock_guard<std::mutex> lock(handle->mutex);
+  handle->probe = slots;
+  handle->probe_capacity = slots ? capacity : 0;
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+int grxblasCycleSlotsNeeded(grxblasHandle_t handle, int m, int n) {
+  (void)handle;
+  const int64_t s = grxk::gemm_probe_slots(m, n);
+  return s > INT_MAX ? INT_MAX : (int)s;
+}
+
+grxblasStatus_t grxblasGetLoadedKernelPath(grxblasHandle_t handle, const char** path) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!path) return GRXBLAS_STATUS_INVALID_VALUE;
+  std::lock_guard<std::mutex> lock(handle->mutex);
+  *path = handle->kernel_path.empty() ? nullptr : handle->kernel_path.c_str();
+  return GRXBLAS_STATUS_SUCCESS;
+}
+
+// ---- level 1 / 2 (ref grxblas.cpp:736-865) ---------------------------------
+
+grxblasStatus_t grxblasSaxpy(grxblasHandle_t handle, int n, const float* alpha, const float* x,
+                             int incx, float* y, int incy) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!alpha) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (n < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (n == 0) return GRXBLAS_STATUS_SUCCESS;
+  if (!x || !y) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (incx == 0 || incy == 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+  return from_hip(grxk::launch_saxpy(n, *alpha, x, incx, y, incy, handle->stream));
+}
+
+grxblasStatus_t grxblasSscal(grxblasHandle_t handle, int n, const float* alpha, float* x,
+                             int incx) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!alpha) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (n < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (n == 0) return GRXBLAS_STATUS_SUCCESS;
+  if (!x) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (incx <= 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+  return from_hip(grxk::launch_sscal(n, *alpha, x, incx, handle->stream));
+}
+
+grxblasStatus_t grxblasSgemv(grxblasHandle_t handle, grxblasOperation_t trans, int m, int n,
+                             const float* alpha, const void* A, int lda, const void* x,
+                             int incx, const float* beta, void* y, int incy) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!alpha || !beta) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m < 0 || n < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m == 0 || n == 0) return GRXBLAS_STATUS_SUCCESS;
+  if (!A || !x || !y) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (incx == 0 || incy == 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (lda < m) return GRXBLAS_STATUS_INVALID_VALUE;
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+  return from_hip(grxk::launch_sgemv(trans == GRXBLAS_OP_T, m, n, *alpha, (const float*)A, lda,
+                                     (const float*)x, incx, *beta, (float*)y, incy,
+                                     handle->stream));
+}
+
+// ---- Sgemm / SgemmStridedBatched: one body (ref grxblas.cpp:867-963) --------
+
+static grxblasStatus_t sgemm_batched(grxblasHandle_t handle, grxblasOperation_t transa,
+                                     grxblasOperation_t transb, int m, int n, int k,
+                                     const float* alpha, const void* A, int lda,
+                                     long long strideA, const void* B, int ldb,
+                                     long long strideB, const float* beta, void* C, int ldc,
+                                     long long strideC, int batch) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!alpha || !beta) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m < 0 || n < 0 || k < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (batch < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m == 0 || n == 0 || batch == 0) return GRXBLAS_STATUS_SUCCESS;
+  if (k > 0 && (!A || !B)) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (!C) return GRXBLAS_STATUS_INVALID_VALUE;
+  const int min_lda = (transa == GRXBLAS_OP_N) ? m : k;
+  const int min_ldb = (transb == GRXBLAS_OP_N) ? k : n;
+  if (lda < min_lda || ldb < min_ldb || ldc < m) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (batch > 65535) return GRXBLAS_STATUS_NOT_SUPPORTED;
+
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+
+  grxCycleSlot* probe = nullptr;
+  const grxblasStatus_t ps =
+      probe_for(*handle, grxk::gemm_probe_slots(m, n) * (int64_t)batch, &probe);
+  if (ps != GRXBLAS_STATUS_SUCCESS) return ps;
+
+  grxk::SgemmDesc d{};
+  d.m = m; d.n = n; d.k = k; d.batch = batch;
+  d.ta = (transa == GRXBLAS_OP_T);
+  d.tb = (transb == GRXBLAS_OP_T);
+  d.a = (const float*)A; d.lda = lda; d.stride_a = strideA;
+  d.b = (const float*)B; d.ldb = ldb; d.stride_b = strideB;
+  d.c = (float*)C; d.ldc = ldc; d.stride_c = strideC;
+  d.alpha = *alpha; d.beta = *beta;
+  d.probe = probe;
+  return from_hip(grxk::launch_sgemm(d, handle->stream));
+}
+
+grxblasStatus_t grxblasSgemm(grxblasHandle_t handle, grxblasOperation_t transa,
+                             grxblasOperation_t transb, int m, int n, int k, const float* alpha,
+                             const void* A, int lda, const void* B, int ldb, const float* beta,
+                             void* C, int ldc) {
+  return sgemm_batched(handle, transa, transb, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C,
+                       ldc, 0, 1);
+}
+
+grxblasStatus_t grxblasSgemmStridedBatched(grxblasHandle_t handle, grxblasOperation_t transa,
+                                           grxblasOperation_t transb, int m, int n, int k,
+                                           const float* alpha, const void* A, int lda,
+                                           long long strideA, const void* B, int ldb,
+                                           long long strideB, const float* beta, void* C,
+                                           int ldc, long long strideC, int batchCount) {
+  return sgemm_batched(handle, transa, transb, m, n, k, alpha, A, lda, strideA, B, ldb, strideB,
+                       beta, C, ldc, strideC, batchCount);
+}
+
+}  // extern "C"

@@ -1,0 +1,512 @@
+// grxBLAS GemmEx on gfx950 matrix cores.
+//
+// Replaces the reference's tensor-unit GEMM (ref: src/libs/grxblas/kernels/
+// hgemm_tcu.cpp:215-372, a single persistent CTA walking 8x4x8 WMMA tiles fed
+// by DXA descriptor copies) with two MFMA kernels:
+//
+//  * gemm_tn_fast: op(A) and op(B) both K-contiguous (transa=T, transb=N in
+//    grxBLAS's column-major terms, i.e. row-major A times column-major B). A
+//    256x256 macro tile per 256-thread workgroup (4 waves, 128x128 each, 4x4
+//    v_mfma 32x32 tiles per wave), 128 bytes of K per stage (64 bf16/fp16 or
+//    128 int8), two LDS stages of 64 KB, 16-byte buffer loads, an XOR swizzle
+//    that keeps ds_read_b128 / ds_write_b128 free of bank conflicts, and an
+//    XCD-aware tile order. Ragged m/n are handled by the buffer descriptor's
+//    range check (out-of-range rows read as zero) plus masked stores; a ragged
+//    k is masked per 16-byte chunk, so k only has to be a multiple of 16 bytes.
+//
+//  * gemm_general: every transpose combination, any m/n/k, any leading
+//    dimension and alignment. 64x64 tiles, element-wise guarded staging into
+//    LDS in the same [row][k] layout the matrix cores read, 4 waves of one
+//    32x32 MFMA tile each. This is the path the reference's ragged and
+//    transposed gate cases exercise.
+//
+// Both kernels are byte-generic: every v_mfma used consumes 16 bytes of A and
+// 16 bytes of B per lane (8 bf16/fp16 or 16 int8) and produces the same 32x32
+// accumulator layout, so one body serves all three input types.
+//
+// Accumulator layout of a 32x32 MFMA (verified on gfx950 by
+// tests/test_gpu_gemm.py): lane l, element r holds row
+// 8*(r/4) + 4*(l/32) + r%4, column l%32.
+
+#include "../launch.h"
+#include "device_common.h"
+
+namespace grxk {
+namespace {
+
+// ---------------------------------------------------------------------------
+// matrix-core ops: 16 bytes of A and B per lane, 32x32 output per wave
+// ---------------------------------------------------------------------------
+
+struct OpBF16 {
+  using Acc = f32x16;
+  using Elem = float;
+  static constexpr int kElemBytes = 2;
+  __device__ static Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct OpF16 {
+  using Acc = f32x16;
+  using Elem = float;
+  static constexpr int kElemBytes = 2;
+  __device__ static Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct OpI8 {
+  using Acc = i32x16;
+  using Elem = int;
+  static constexpr int kElemBytes = 1;
+  __device__ static Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+};
+
+struct KParams {
+  const uint8_t* a;
+  const uint8_t* b;
+  void* c;
+  int64_t lda, ldb, ldc;  // elements
+  int m, n, k;
+  int tiles_m, tiles_n;
+  int ta, tb;             // general kernel only
+  float alpha, beta;
+  int32_t ialpha, ibeta;
+  const float* scale;
+  grxCycleSlot* probe;
+};
+
+// ---------------------------------------------------------------------------
+// epilogue: 4 consecutive rows i0..i0+3 of column j
+// ---------------------------------------------------------------------------
+
+template <MmaOut OUT>
+struct Epi;
+
+template <>
+struct Epi<MmaOut::F32> {
+  __device__ static float apply(const KParams& p, float acc, float c_old) {
+    // alpha*acc (+ beta*C) with each operation rounded separately, as the
+    // reference's CPU gate writes it (no contraction into an FMA).
+    const float s = __fmul_rn(p.alpha, acc);
+    return p.beta == 0.0f ? s : __fadd_rn(s, __fmul_rn(p.beta, c_old));
+  }
+  __device__ static void store4(const KParams& p, int i0, int j, const float v[4], bool vec) {
+    float* c = (float*)p.c + (int64_t)j * p.ldc + i0;
+    if (vec) {
+      f32x4 old = {0, 0, 0, 0};
+      if (p.beta != 0.0f) old = *(const f32x4*)c;
+      f32x4 o;
+      o.x = apply(p, v[0], old.x); o.y = apply(p, v[1], old.y);
+      o.z = apply(p, v[2], old.z); o.w = apply(p, v[3], old.w);
+      *(f32x4*)c = o;
+    } else {
+      for (int q = 0; q < 4; ++q)
+        if (i0 + q < p.m) c[q] = apply(p, v[q], p.beta != 0.0f ? c[q] : 0.0f);
+    }
+  }
+};
+
+template <MmaOut OUT>
+struct EpiNarrow {
+  __device__ static uint16_t cvt(float x) {
+    if constexpr (OUT == MmaOut::BF16) return f32_to_bf16(x);
+    else return f32_to_f16(x);
+  }
+  __device__ static float back(uint16_t x) {
+    if constexpr (OUT == MmaOut::BF16) return bf16_to_f32(x);
+    else return f16_to_f32(x);
+  }
+  __device__ static float apply(const KParams& p, float acc, uint16_t c_old) {
+    const float s = __fmul_rn(p.alpha, acc);
+    return p.beta == 0.0f ? s : __fadd_rn(s, __fmul_rn(p.beta, back(c_old)));
+  }
+  __device__ static void store4(const KParams& p, int i0, int j, const float v[4], bool vec) {
+    uint16_t* c = (uint16_t*)p.c + (int64_t)j * p.ldc + i0;
+    if (vec) {
+      u32x2 old = {0, 0};
+      if (p.beta != 0.0f) old = *(const u32x2*)c;
+      u32x2 o;
+      o.x = (uint32_t)cvt(apply(p, v[0], (uint16_t)(old.x & 0xffff))) |
+            ((uint32_t)cvt(apply(p, v[1], (uint16_t)(old.x >> 16))) << 16);
+      o.y = (uint32_t)cvt(apply(p, v[2], (uint16_t)(old.y & 0xffff))) |
+            ((uint32_t)cvt(apply(p, v[3], (uint16_t)(old.y >> 16))) << 16);
+      *(u32x2*)c = o;
+    } else {
+      for (int q = 0; q < 4; ++q)
+        if (i0 + q < p.m) c[q] = cvt(apply(p, v[q], p.beta != 0.0f ? c[q] : (uint16_t)0));
+    }
+  }
+};
+template <> struct Epi<MmaOut::BF16> : EpiNarrow<MmaOut::BF16> {};
+template <> struct Epi<MmaOut::F16> : EpiNarrow<MmaOut::F16> {};
+
+template <>
+struct Epi<MmaOut::I32> {
+  __device__ static int apply(const KParams& p, int acc, int c_old) {
+    uint32_t r = (uint32_t)p.ialpha * (uint32_t)acc;
+    if (p.ibeta != 0) r += (uint32_t)p.ibeta * (uint32_t)c_old;
+    return (int)r;
+  }
+  __device__ static void store4(const KParams& p, int i0, int j, const int v[4], bool vec) {
+    int* c = (int*)p.c + (int64_t)j * p.ldc + i0;
+    if (vec) {
+      i32x4 old = {0, 0, 0, 0};
+      if (p.ibeta != 0) old = *(const i32x4*)c;
+      i32x4 o;
+      o.x = apply(p, v[0], old.x); o.y = apply(p, v[1], old.y);
+      o.z = apply(p, v[2], old.z); o.w = apply(p, v[3], old.w);
+      *(i32x4*)c = o;
+    } else {
+      for (int q = 0; q < 4; ++q)
+        if (i0 + q < p.m) c[q] = apply(p, v[q], p.ibeta != 0 ? c[q] : 0);
+    }
+  }
+};
+
+template <>
+struct Epi<MmaOut::DEQ_BF16> {
+  // bf16_rne(f32_rne(f32_rne(acc) * scale[j])): v_cvt_f32_i32 rounds to
+  // nearest even, __fmul_rn is one correctly rounded product.
+  __device__ static uint16_t apply(float s, int acc) {
+    return f32_to_bf16(__fmul_rn((float)acc, s));
+  }
+  __device__ static void store4(const KParams& p, int i0, int j, const int v[4], bool vec) {
+    uint16_t* c = (uint16_t*)p.c + (int64_t)j * p.ldc + i0;
+    const float s = p.scale[j];
+    if (vec) {
+      u32x2 o;
+      o.x = (uint32_t)apply(s, v[0]) | ((uint32_t)apply(s, v[1]) << 16);
+      o.y = (uint32_t)apply(s, v[2]) | ((uint32_t)apply(s, v[3]) << 16);
+      *(u32x2*)c = o;
+    } else {
+      for (int q = 0; q < 4; ++q)
+        if (i0 + q < p.m) c[q] = apply(s, v[q]);
+    }
+  }
+};
+
+// Spread a 32x32 accumulator tile (rows base_i.., cols base_j..) to C.
+template <class Op, MmaOut OUT>
+__device__ __forceinline__ void store_acc_tile(const KParams& p, const typename Op::Acc& acc,
+                                               int base_i, int base_j, int lane, bool vec_ok) {
+  using E = typename Op::Elem;
+  const int j = base_j + (lane & 31);
+  if (j >= p.n) return;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int i0 = base_i + 8 * g + 4 * (lane >> 5);
+    if (i0 >= p.m) continue;
+    E v[4] = {(E)acc[4 * g + 0], (E)acc[4 * g + 1], (E)acc[4 * g + 2], (E)acc[4 * g + 3]};
+    Epi<OUT>::store4(p, i0, j, v, vec_ok && (i0 + 3 < p.m));
+  }
+}
+
+// XCD-aware tile order. Consecutive workgroup ids are dispatched round-robin
+// over the 8 XCDs; remapping gives each XCD a contiguous run of logical tiles,
+// and the logical order walks groups of 8 tile-rows so that neighbours share
+// A panels in that XCD's L2.
+__device__ __forceinline__ void map_tile(int bid, int nblocks, int tiles_m, int tiles_n,
+                                         int& tm, int& tn) {
+  int logical = bid;
+  if ((nblocks & 7) == 0) logical = (bid & 7) * (nblocks >> 3) + (bid >> 3);
+  constexpr int kGroup = 8;
+  const int per_group = kGroup * tiles_n;
+  const int group = logical / per_group;
+  const int first_m = group * kGroup;
+  const int gsize = min(tiles_m - first_m, kGroup);
+  const int in_group = logical - group * per_group;
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+// ---------------------------------------------------------------------------
+// TN fast path
+// ---------------------------------------------------------------------------
+
+constexpr int kFastTile = 256;   // rows of op(A) and columns of op(B) per workgroup
+constexpr int kFastKBytes = 128; // bytes of K per stage
+constexpr int kChunks = kFastKBytes / 16;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
+
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+template <class Op, MmaOut OUT>
+__global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
+  __shared__ __attribute__((aligned(16))) i32x4 lds[2][2][kFastTile * kChunks];
+
+  const uint64_t t0 = p.probe ? cycle_now() : 0;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  int tm, tn;
+  map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int row0 = tm * kFastTile;
+  const int col0 = tn * kFastTile;
+
+  const int64_t lda_b = p.lda * Op::kElemBytes;
+  const int64_t ldb_b = p.ldb * Op::kElemBytes;
+  const int kbytes = p.k * Op::kElemBytes;
+  const int ktiles = (kbytes + kFastKBytes - 1) / kFastKBytes;
+
+  // Buffer descriptors start at this tile's first row; the record count ends
+  // at row m (n), so rows past the matrix read as zero without a branch.
+  const int rows_a = min(kFastTile, p.m - row0);
+  const int rows_b = min(kFastTile, p.n - col0);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.a + (int64_t)row0 * lda_b), (short)0,
+      (int)((int64_t)(rows_a - 1) * lda_b + kbytes), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.b + (int64_t)col0 * ldb_b), (short)0,
+      (int)((int64_t)(rows_b - 1) * ldb_b + kbytes), kRsrcWord3);
+
+  // Loader: thread t moves 16-byte chunk (t & 7) of rows (t >> 3) + 32*i.
+  const int lrow = tid >> 3;
+  const int lch = tid & 7;
+  const uint32_t voff_a = (uint32_t)(lrow * lda_b + lch * 16);
+  const uint32_t voff_b = (uint32_t)(lrow * ldb_b + lch * 16);
+  const uint32_t step_a = (uint32_t)(32 * lda_b);
+  const uint32_t step_b = (uint32_t)(32 * ldb_b);
+
+  i32x4 ga[8], gb[8];
+  auto load_stage = [&](int kt) {
+    const int kb = kt * kFastKBytes;
+    const bool kvalid = kb + lch * 16 < kbytes;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ga[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, voff_a + i * step_a + kb, 0, 0);
+      gb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, voff_b + i * step_b + kb, 0, 0);
+      if (!kvalid) { ga[i] = i32x4{0, 0, 0, 0}; gb[i] = i32x4{0, 0, 0, 0}; }
+    }
+  };
+  auto store_stage = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = lrow + 32 * i;
+      const int slot = row * kChunks + (lch ^ swz(row));
+      lds[st][0][slot] = ga[i];
+      lds[st][1][slot] = gb[i];
+    }
+  };
+
+  using Acc = typename Op::Acc;
+  Acc acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int r32 = lane & 31;
+  const int hh = lane >> 5;
+
+  if (ktiles > 0) {
+    load_stage(0);
+    store_stage(0);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ktiles;
+    if (more) load_stage(kt + 1);
+
+#pragma unroll
+    for (int ks = 0; ks < kChunks / 2; ++ks) {
+      const int kc = 2 * ks + hh;
+      i32x4 fa[4], fb[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int ra_row = wm * 128 + t * 32 + r32;
+        const int rb_row = wn * 128 + t * 32 + r32;
+        fa[t] = lds[cur][0][ra_row * kChunks + (kc ^ swz(ra_row))];
+        fb[t] = lds[cur][1][rb_row * kChunks + (kc ^ swz(rb_row))];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = Op::mma(fa[i], fb[j], acc[i][j]);
+    }
+
+    if (more) store_stage(cur ^ 1);
+    __syncthreads();
+  }
+
+  const bool vec_ok = true;  // host guarantees ldc % 8 == 0 and an aligned C
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      store_acc_tile<Op, OUT>(p, acc[i][j], row0 + wm * 128 + i * 32, col0 + wn * 128 + j * 32,
+                              lane, vec_ok);
+
+  cycle_record(p.probe, t0, blockIdx.x * 4 + wave, wave);
+}
+
+// ---------------------------------------------------------------------------
+// general path
+// ---------------------------------------------------------------------------
+
+constexpr int kGenTile = 64;
+constexpr int kGenKBytes = 64;                 // two MFMA k-steps per stage
+constexpr int kGenRowBytes = kGenKBytes + 16;  // padded row: conflict-free b128 reads
+
+template <class Op, MmaOut OUT>
+__global__ __launch_bounds__(256) void gemm_general(KParams p) {
+  constexpr int EB = Op::kElemBytes;
+  constexpr int KT = kGenKBytes / EB;  // elements of K per stage
+  __shared__ __attribute__((aligned(16))) uint8_t sa[kGenTile * kGenRowBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t sb[kGenTile * kGenRowBytes];
+
+  const uint64_t t0 = p.probe ? cycle_now() : 0;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tm = blockIdx.x % p.tiles_m;
+  const int tn = blockIdx.x / p.tiles_m;
+  const int row0 = tm * kGenTile;
+  const int col0 = tn * kGenTile;
+
+  using Acc = typename Op::Acc;
+  Acc acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0;
+
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ktiles = (p.k + KT - 1) / KT;
+  constexpr int kPerThread = kGenTile * KT / 256;
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int k0 = kt * KT;
+    // Stage op(A)[row0.., k0..] as [row][k] and op(B)[k0.., col0..] as [col][k].
+    // The thread -> element map follows the operand's contiguous dimension so
+    // that global reads coalesce.
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q) {
+      const int e = tid + 256 * q;
+      int r, kk;
+      if (p.ta) { r = e / KT; kk = e % KT; } else { kk = e / kGenTile; r = e % kGenTile; }
+      const int gi = row0 + r, gk = k0 + kk;
+      uint8_t* dst = sa + r * kGenRowBytes + kk * EB;
+      if (gi < p.m && gk < p.k) {
+        const int64_t off = p.ta ? ((int64_t)gi * p.lda + gk) : ((int64_t)gk * p.lda + gi);
+        if constexpr (EB == 2) *(uint16_t*)dst = ((const uint16_t*)p.a)[off];
+        else *dst = p.a[off];
+      } else {
+        if constexpr (EB == 2) *(uint16_t*)dst = 0;
+        else *dst = 0;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q) {
+      const int e = tid + 256 * q;
+      int c, kk;
+      if (!p.tb) { c = e / KT; kk = e % KT; } else { kk = e / kGenTile; c = e % kGenTile; }
+      const int gj = col0 + c, gk = k0 + kk;
+      uint8_t* dst = sb + c * kGenRowBytes + kk * EB;
+      if (gj < p.n && gk < p.k) {
+        const int64_t off = p.tb ? ((int64_t)gk * p.ldb + gj) : ((int64_t)gj * p.ldb + gk);
+        if constexpr (EB == 2) *(uint16_t*)dst = ((const uint16_t*)p.b)[off];
+        else *dst = p.b[off];
+      } else {
+        if constexpr (EB == 2) *(uint16_t*)dst = 0;
+        else *dst = 0;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kGenKBytes / 32; ++ks) {
+      const int kb = ks * 32 + (lane >> 5) * 16;
+      const i32x4 fa = *(const i32x4*)(sa + (wm * 32 + (lane & 31)) * kGenRowBytes + kb);
+      const i32x4 fb = *(const i32x4*)(sb + (wn * 32 + (lane & 31)) * kGenRowBytes + kb);
+      acc = Op::mma(fa, fb, acc);
+    }
+    __syncthreads();
+  }
+
+  store_acc_tile<Op, OUT>(p, acc, row0 + wm * 32, col0 + wn * 32, lane, false);
+  cycle_record(p.probe, t0, blockIdx.x * 4 + wave, wave);
+}
+
+// ---------------------------------------------------------------------------
+// dispatch
+// ---------------------------------------------------------------------------
+
+template <class Op, MmaOut OUT>
+hipError_t run(const GemmDesc& d, hipStream_t s) {
+  KParams p{};
+  p.a = (const uint8_t*)d.a;
+  p.b = (const uint8_t*)d.b;
+  p.c = d.c;
+  p.lda = d.lda; p.ldb = d.ldb; p.ldc = d.ldc;
+  p.m = d.m; p.n = d.n; p.k = d.k;
+  p.ta = d.ta; p.tb = d.tb;
+  p.alpha = d.alpha; p.beta = d.beta;
+  p.ialpha = d.ialpha; p.ibeta = d.ibeta;
+  p.scale = d.scale;
+  p.probe = d.probe;
+
+  constexpr int EB = Op::kElemBytes;
+  const int out_bytes = (OUT == MmaOut::F32 || OUT == MmaOut::I32) ? 4 : 2;
+  // The fast path needs K-contiguous operands whose rows start on 16-byte
+  // boundaries (so every staged chunk is one aligned 16-byte load), 32-bit
+  // buffer offsets within a 256-row panel, and a C whose 4-row groups are
+  // aligned for one vector store.
+  const bool fast =
+      d.ta && !d.tb && d.k > 0 &&
+      ((int64_t)d.k * EB) % 16 == 0 &&
+      (d.lda * EB) % 16 == 0 && (d.ldb * EB) % 16 == 0 &&
+      ((uintptr_t)d.a % 16) == 0 && ((uintptr_t)d.b % 16) == 0 &&
+      d.ldc % 8 == 0 && ((uintptr_t)d.c % (4 * out_bytes)) == 0 &&
+      (int64_t)kFastTile * d.lda * EB < (1ll << 31) &&
+      (int64_t)kFastTile * d.ldb * EB < (1ll << 31);
+  if (fast) {
+    p.tiles_m = (d.m + kFastTile - 1) / kFastTile;
+    p.tiles_n = (d.n + kFastTile - 1) / kFastTile;
+    const int blocks = p.tiles_m * p.tiles_n;
+    hipLaunchKernelGGL((gemm_tn_fast<Op, OUT>), dim3(blocks), dim3(256), 0, s, p);
+  } else {
+    p.tiles_m = (d.m + kGenTile - 1) / kGenTile;
+    p.tiles_n = (d.n + kGenTile - 1) / kGenTile;
+    const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemm_general<Op, OUT>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int64_t gemm_probe_slots(int m, int n) {
+  if (m <= 0 || n <= 0) return 0;
+  return ((int64_t)(m + kGenTile - 1) / kGenTile) * ((n + kGenTile - 1) / kGenTile) * 4;
+}
+
+hipError_t launch_mma_gemm(MmaIn in, MmaOut out, const GemmDesc& d, hipStream_t s) {
+  switch (in) {
+    case MmaIn::BF16:
+      if (out == MmaOut::F32) return run<OpBF16, MmaOut::F32>(d, s);
+      if (out == MmaOut::BF16) return run<OpBF16, MmaOut::BF16>(d, s);
+      break;
+    case MmaIn::F16:
+      if (out == MmaOut::F32) return run<OpF16, MmaOut::F32>(d, s);
+      if (out == MmaOut::F16) return run<OpF16, MmaOut::F16>(d, s);
+      break;
+    case MmaIn::I8:
+      if (out == MmaOut::I32) return run<OpI8, MmaOut::I32>(d, s);
+      if (out == MmaOut::DEQ_BF16) return run<OpI8, MmaOut::DEQ_BF16>(d, s);
+      break;
+  }
+  return hipErrorNotSupported;
+}
+
+}  // namespace grxk

@@ -1,0 +1,261 @@
+// grxDNN RMSNorm / LayerNorm forward on gfx950.
+//
+// New (the reference plans grxDNN normalisation but ships none:
+// ref docs/designs/grxcp_roadmap.md:864-877). HBM-bound: every byte of x is
+// read once and every byte of y written once, so the design goal is streaming
+// bandwidth, not arithmetic.
+//
+//  * one row per 256-thread workgroup (4 wavefronts); thousands of rows give
+//    far more than the 256 CUs x 8 resident workgroups needed to keep HBM busy;
+//  * the row is held in registers between the statistics pass and the output
+//    pass (up to 8 x 16-byte chunks per thread = 16384 bf16 elements), so x is
+//    read from HBM exactly once; longer rows re-read x (from L2);
+//  * 16-byte non-temporal loads of x and stores of y, gamma/beta via the
+//    normal cached path (every row reuses them);
+//  * statistics in fp32: wavefront butterfly (__shfl_xor) then a 4-entry LDS
+//    combine, summed in a fixed order so every thread sees the same value.
+//    LayerNorm's variance is the two-pass (x - mean)^2 form over the cached
+//    registers, which costs no extra memory traffic.
+// Rows whose length, pitch or base alignment rule out 16-byte chunks take a
+// scalar path with the same arithmetic.
+
+#include "../launch.h"
+#include "device_common.h"
+
+namespace grxk {
+namespace {
+
+struct NParams {
+  const uint8_t* x;
+  const uint8_t* gamma;
+  const uint8_t* beta;
+  uint8_t* y;
+  int64_t x_rs, y_rs;  // row strides, elements
+  int64_t rows;
+  int hidden;
+  float eps;
+};
+
+template <NormType T> struct Io;
+template <> struct Io<NormType::BF16> {
+  static constexpr int kVec = 8;
+  __device__ static float ld(const uint8_t* p, int64_t i) { return bf16_to_f32(((const uint16_t*)p)[i]); }
+  __device__ static void st(uint8_t* p, int64_t i, float v) { ((uint16_t*)p)[i] = f32_to_bf16(v); }
+  __device__ static void unpack(const u32x4 w, float* f) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f[2 * q] = __uint_as_float(w[q] << 16);
+      f[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+    }
+  }
+  __device__ static u32x4 pack(const float* f) {
+    u32x4 w;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
+    return w;
+  }
+};
+template <> struct Io<NormType::F16> {
+  static constexpr int kVec = 8;
+  __device__ static float ld(const uint8_t* p, int64_t i) { return f16_to_f32(((const uint16_t*)p)[i]); }
+  __device__ static void st(uint8_t* p, int64_t i, float v) { ((uint16_t*)p)[i] = f32_to_f16(v); }
+  __device__ static void unpack(const u32x4 w, float* f) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f[2 * q] = f16_to_f32((uint16_t)(w[q] & 0xffffu));
+      f[2 * q + 1] = f16_to_f32((uint16_t)(w[q] >> 16));
+    }
+  }
+  __device__ static u32x4 pack(const float* f) {
+    u32x4 w;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w[q] = (uint32_t)f32_to_f16(f[2 * q]) | ((uint32_t)f32_to_f16(f[2 * q + 1]) << 16);
+    return w;
+  }
+};
+template <> struct Io<NormType::F32> {
+  static constexpr int kVec = 4;
+  __device__ static float ld(const uint8_t* p, int64_t i) { return ((const float*)p)[i]; }
+  __device__ static void st(uint8_t* p, int64_t i, float v) { ((float*)p)[i] = v; }
+  __device__ static void unpack(const u32x4 w, float* f) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f[q] = __uint_as_float(w[q]);
+  }
+  __device__ static u32x4 pack(const float* f) {
+    u32x4 w;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = __float_as_uint(f[q]);
+    return w;
+  }
+};
+
+// Sum over the 256-thread workgroup, identical in every thread.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();  // red[] may still be read from a previous reduction
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <NormType T, bool LAYER, int NQ>
+__global__ __launch_bounds__(256) void norm_vec(NParams p) {
+  using IO = Io<T>;
+  constexpr int V = IO::kVec;
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int nchunks = p.hidden / V;
+  const float inv_h = 1.0f / (float)p.hidden;
+
+  for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
+    const uint8_t* xrow = p.x + row * p.x_rs * (int64_t)(16 / V);
+    uint8_t* yrow = p.y + row * p.y_rs * (int64_t)(16 / V);
+
+    float v[NQ][V];
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = tid + 256 * q;
+      if (c < nchunks) {
+        const u32x4 w = __builtin_nontemporal_load((const u32x4*)xrow + c);
+        IO::unpack(w, v[q]);
+#pragma unroll
+        for (int e = 0; e < V; ++e) s += LAYER ? v[q][e] : v[q][e] * v[q][e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[q][e] = 0.0f;
+      }
+    }
+    s = block_sum(s, red);
+    float mean = 0.0f, inv;
+    if (LAYER) {
+      mean = s * inv_h;
+      float d2 = 0.0f;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int c = tid + 256 * q;
+        if (c < nchunks) {
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            const float d = v[q][e] - mean;
+            d2 += d * d;
+          }
+        }
+      }
+      d2 = block_sum(d2, red);
+      inv = 1.0f / sqrtf(d2 * inv_h + p.eps);
+    } else {
+      inv = 1.0f / sqrtf(s * inv_h + p.eps);
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = tid + 256 * q;
+      if (c < nchunks) {
+        float g[V], o[V];
+        IO::unpack(((const u32x4*)p.gamma)[c], g);
+        if (LAYER) {
+          float b[V];
+          IO::unpack(((const u32x4*)p.beta)[c], b);
+#pragma unroll
+          for (int e = 0; e < V; ++e) o[e] = (v[q][e] - mean) * inv * g[e] + b[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) o[e] = v[q][e] * inv * g[e];
+        }
+        __builtin_nontemporal_store(IO::pack(o), (u32x4*)yrow + c);
+      }
+    }
+  }
+}
+
+// Any length / alignment: element-wise, x re-read for each pass.
+template <NormType T, bool LAYER>
+__global__ __launch_bounds__(256) void norm_scalar(NParams p) {
+  using IO = Io<T>;
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const float inv_h = 1.0f / (float)p.hidden;
+  for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
+    const int64_t xo = row * p.x_rs, yo = row * p.y_rs;
+    float s = 0.0f;
+    for (int c = tid; c < p.hidden; c += 256) {
+      const float x = IO::ld(p.x, xo + c);
+      s += LAYER ? x : x * x;
+    }
+    s = block_sum(s, red);
+    float mean = 0.0f, inv;
+    if (LAYER) {
+      mean = s * inv_h;
+      float d2 = 0.0f;
+      for (int c = tid; c < p.hidden; c += 256) {
+        const float d = IO::ld(p.x, xo + c) - mean;
+        d2 += d * d;
+      }
+      d2 = block_sum(d2, red);
+      inv = 1.0f / sqrtf(d2 * inv_h + p.eps);
+    } else {
+      inv = 1.0f / sqrtf(s * inv_h + p.eps);
+    }
+    for (int c = tid; c < p.hidden; c += 256) {
+      const float x = IO::ld(p.x, xo + c);
+      const float g = IO::ld(p.gamma, c);
+      const float o = LAYER ? (x - mean) * inv * g + IO::ld(p.beta, c) : x * inv * g;
+      IO::st(p.y, yo + c, o);
+    }
+  }
+}
+
+template <NormType T, bool LAYER>
+hipError_t run(const NormDesc& d, hipStream_t s) {
+  NParams p{};
+  p.x = (const uint8_t*)d.x;
+  p.gamma = (const uint8_t*)d.gamma;
+  p.beta = (const uint8_t*)d.beta;
+  p.y = (uint8_t*)d.y;
+  p.x_rs = d.x_row_stride;
+  p.y_rs = d.y_row_stride;
+  p.rows = d.rows;
+  p.hidden = d.hidden;
+  p.eps = d.eps;
+  constexpr int V = Io<T>::kVec;
+  const unsigned grid = (unsigned)std::min<int64_t>(d.rows, 1 << 30);
+  auto al = [](const void* q) { return ((uintptr_t)q % 16) == 0; };
+  const bool vec = d.hidden % V == 0 && d.x_row_stride % V == 0 && d.y_row_stride % V == 0 &&
+                   al(d.x) && al(d.y) && al(d.gamma) && (!LAYER || al(d.beta));
+  const int nchunks = d.hidden / V;
+  if (vec && nchunks <= 256) {
+    hipLaunchKernelGGL((norm_vec<T, LAYER, 1>), dim3(grid), dim3(256), 0, s, p);
+  } else if (vec && nchunks <= 512) {
+    hipLaunchKernelGGL((norm_vec<T, LAYER, 2>), dim3(grid), dim3(256), 0, s, p);
+  } else if (vec && nchunks <= 1024) {
+    hipLaunchKernelGGL((norm_vec<T, LAYER, 4>), dim3(grid), dim3(256), 0, s, p);
+  } else if (vec && nchunks <= 2048) {
+    hipLaunchKernelGGL((norm_vec<T, LAYER, 8>), dim3(grid), dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((norm_scalar<T, LAYER>), dim3(grid), dim3(256), 0, s, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(NormType t, const NormDesc& d, hipStream_t s) {
+  switch (t) {
+    case NormType::BF16: return run<NormType::BF16, false>(d, s);
+    case NormType::F16:  return run<NormType::F16, false>(d, s);
+    case NormType::F32:  return run<NormType::F32, false>(d, s);
+  }
+  return hipErrorNotSupported;
+}
+
+hipError_t launch_layernorm(NormType t, const NormDesc& d, hipStream_t s) {
+  switch (t) {
+    case NormType::BF16: return run<NormType::BF16, true>(d, s);
+    case NormType::F16:  return run<NormType::F16, true>(d, s);
+    case NormType::F32:  return run<NormType::F32, true>(d, s);
+  }
+  return hipErrorNotSupported;
+}
+
+}  // namespace grxk

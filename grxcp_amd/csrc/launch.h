@@ -1,0 +1,87 @@
+// Internal interface between the host libraries (argument validation, status
+// mapping) and the gfx950 kernels (one launcher per kernel family). Nothing
+// here is exported from the shared libraries.
+#ifndef GRXCP_LAUNCH_H
+#define GRXCP_LAUNCH_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include <grx/grx_cycles.h>
+
+namespace grxk {
+
+// Element types the matrix-core GEMM reads and the epilogue it ends in.
+enum class MmaIn { BF16, F16, I8 };
+enum class MmaOut {
+  F32,        // alpha*acc + beta*C, fp32 C
+  BF16,       // same, rounded to bf16 (RNE)
+  F16,        // same, rounded to fp16 (RNE)
+  I32,        // integral alpha/beta in int32, wrapping
+  DEQ_BF16    // bf16(f32(acc) * scale[col])
+};
+
+struct GemmDesc {
+  int m, n, k;
+  bool ta, tb;              // op(A) = A^T / op(B) = B^T
+  const void* a; int64_t lda;
+  const void* b; int64_t ldb;
+  void* c;       int64_t ldc;
+  float alpha, beta;        // floating epilogues
+  int32_t ialpha, ibeta;    // integer epilogue
+  const float* scale;       // DEQ_BF16
+  grxCycleSlot* probe;      // may be null
+};
+
+// Picks the kernel (TN fast path or general path) and launches it.
+hipError_t launch_mma_gemm(MmaIn in, MmaOut out, const GemmDesc& d, hipStream_t s);
+// Upper bound of probe slots any GEMM launch for an m x n output uses.
+int64_t gemm_probe_slots(int m, int n);
+
+struct SgemmDesc {
+  int m, n, k, batch;
+  bool ta, tb;
+  const float* a; int64_t lda; int64_t stride_a;
+  const float* b; int64_t ldb; int64_t stride_b;
+  float* c;       int64_t ldc; int64_t stride_c;
+  float alpha, beta;
+  grxCycleSlot* probe;
+};
+hipError_t launch_sgemm(const SgemmDesc& d, hipStream_t s);
+
+// Level 1/2, fp32.
+hipError_t launch_saxpy(int n, float alpha, const float* x, int incx, float* y,
+                        int incy, hipStream_t s);
+hipError_t launch_sscal(int n, float alpha, float* x, int incx, hipStream_t s);
+hipError_t launch_sgemv(bool trans, int m, int n, float alpha, const float* A,
+                        int lda, const float* x, int incx, float beta, float* y,
+                        int incy, hipStream_t s);
+
+// grxDNN.
+enum class NormType { BF16, F16, F32 };
+struct NormDesc {
+  int64_t rows;
+  int hidden;
+  int64_t x_row_stride, y_row_stride;  // elements
+  const void* x; const void* gamma; const void* beta;  // beta: LayerNorm only
+  void* y;
+  float eps;
+};
+hipError_t launch_rmsnorm(NormType t, const NormDesc& d, hipStream_t s);
+hipError_t launch_layernorm(NormType t, const NormDesc& d, hipStream_t s);
+
+enum class AttnType { BF16, F16 };
+struct AttnDesc {
+  int B, H, S, D;
+  bool causal;
+  float scale;
+  const void* q; int64_t q_sb, q_sh, q_ss;   // strides (elements) of b, h, s
+  const void* k; int64_t k_sb, k_sh, k_ss;
+  const void* v; int64_t v_sb, v_sh, v_ss;
+  void* o;       int64_t o_sb, o_sh, o_ss;
+};
+hipError_t launch_attention(AttnType t, const AttnDesc& d, hipStream_t s);
+
+}  // namespace grxk
+
+#endif  // GRXCP_LAUNCH_H

@@ -1,0 +1,121 @@
+/* grxdnn.h -- grxDNN forward primitives, MI355X (gfx950) build.
+ *
+ * The reference plans grxDNN but ships no code for it: a CMake slot
+ * (ref: src/libs/CMakeLists.txt:12), an architecture entry naming grxdnn.h
+ * (ref: docs/designs/grxcp_architecture.md:594, 640) and roadmap phase 6
+ * (ref: docs/designs/grxcp_roadmap.md:864-877: "softmax, layernorm, ...,
+ * attention; grxBLAS + custom kernels"). This header is therefore designed
+ * new, in grxBLAS's style (ref: include/grx/grxblas.h): an opaque handle with
+ * a borrowed stream, status codes with grxBLAS's values, device pointers for
+ * tensors, host values for scalars, asynchronous calls, validation before any
+ * device work and NOT_SUPPORTED instead of a silent fallback.
+ *
+ * Tensors are described cuDNN-style by an N-d descriptor (type, dims,
+ * strides in elements). The innermost dimension must have stride 1.
+ */
+#ifndef GRXDNN_H
+#define GRXDNN_H
+
+#include "grx_runtime.h"
+#include "grx_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct grxdnnContext*          grxdnnHandle_t;
+typedef struct grxdnnTensorStruct*     grxdnnTensorDescriptor_t;
+typedef struct grxdnnAttentionStruct*  grxdnnAttentionDescriptor_t;
+
+/* Same values as grxblasStatus_t (ref include/grx/grxblas.h:37-46). */
+typedef enum {
+  GRXDNN_STATUS_SUCCESS          = 0,
+  GRXDNN_STATUS_NOT_INITIALIZED  = 1,
+  GRXDNN_STATUS_ALLOC_FAILED     = 2,
+  GRXDNN_STATUS_INVALID_VALUE    = 3,
+  GRXDNN_STATUS_ARCH_MISMATCH    = 4,
+  GRXDNN_STATUS_EXECUTION_FAILED = 5,
+  GRXDNN_STATUS_NOT_SUPPORTED    = 6,
+  GRXDNN_STATUS_INTERNAL_ERROR   = 7
+} grxdnnStatus_t;
+
+#define GRXDNN_DIM_MAX 8
+
+const char* grxdnnGetStatusString(grxdnnStatus_t s);
+
+grxdnnStatus_t grxdnnCreate   (grxdnnHandle_t* handle);
+grxdnnStatus_t grxdnnDestroy  (grxdnnHandle_t handle);
+grxdnnStatus_t grxdnnSetStream(grxdnnHandle_t handle, grxStream_t stream);
+grxdnnStatus_t grxdnnGetStream(grxdnnHandle_t handle, grxStream_t* stream);
+
+/* ---- tensor descriptors ------------------------------------------------- */
+grxdnnStatus_t grxdnnCreateTensorDescriptor (grxdnnTensorDescriptor_t* desc);
+grxdnnStatus_t grxdnnDestroyTensorDescriptor(grxdnnTensorDescriptor_t desc);
+/* 1 <= nbDims <= GRXDNN_DIM_MAX; dims >= 0; strides >= 0 in elements.
+ * strides may be NULL for a packed (row-major, last dimension contiguous)
+ * layout. */
+grxdnnStatus_t grxdnnSetTensorNdDescriptor(grxdnnTensorDescriptor_t desc,
+                                           grxDataType_t dataType, int nbDims,
+                                           const int dims[],
+                                           const int strides[]);
+grxdnnStatus_t grxdnnGetTensorNdDescriptor(grxdnnTensorDescriptor_t desc,
+                                           int nbDimsRequested,
+                                           grxDataType_t* dataType,
+                                           int* nbDims, int dims[],
+                                           int strides[]);
+
+/* ---- normalisation ------------------------------------------------------
+ * x, y: [..., hidden]; every dimension but the last is a row index, the last
+ * is normalised. The row dimensions must flatten to one row stride (packed
+ * rows, or rows padded by a constant pitch). gamma/beta: 1-d [hidden],
+ * contiguous, same type as x. Supported types: GRX_R_16BF, GRX_R_16F,
+ * GRX_R_32F, with y of the same type and shape as x. Reductions are fp32.
+ *
+ *   RMSNorm:   y = x * rsqrt(mean(x^2) + eps) * gamma
+ *   LayerNorm: y = (x - mean(x)) * rsqrt(var(x) + eps) * gamma + beta
+ *              (biased variance)
+ * eps must be finite and >= 0. hidden must be >= 1 and <= 65536. */
+grxdnnStatus_t grxdnnRMSNormForward(grxdnnHandle_t handle,
+                                    grxdnnTensorDescriptor_t xDesc,
+                                    const void* x,
+                                    grxdnnTensorDescriptor_t wDesc,
+                                    const void* gamma, float eps,
+                                    grxdnnTensorDescriptor_t yDesc, void* y);
+
+grxdnnStatus_t grxdnnLayerNormForward(grxdnnHandle_t handle,
+                                      grxdnnTensorDescriptor_t xDesc,
+                                      const void* x,
+                                      grxdnnTensorDescriptor_t wDesc,
+                                      const void* gamma, const void* beta,
+                                      float eps,
+                                      grxdnnTensorDescriptor_t yDesc, void* y);
+
+/* ---- fused scaled-dot-product attention (forward) ----------------------
+ *
+ *   O[b,h,i,:] = sum_j softmax_j( scale * <Q[b,h,i,:], K[b,h,j,:]> + mask ) V[b,h,j,:]
+ *
+ * with mask = -inf for j > i when causal (the query and key sequences have
+ * the same length and are aligned at position 0). Q, K, V, O are 4-d
+ * [B, H, S, D] descriptors of one type (GRX_R_16BF or GRX_R_16F), innermost
+ * stride 1, with equal B, H, S and D. Supported head dimensions: 64, 128.
+ * Softmax and both products accumulate in fp32; O is rounded once (RNE). */
+grxdnnStatus_t grxdnnCreateAttentionDescriptor (grxdnnAttentionDescriptor_t* d);
+grxdnnStatus_t grxdnnDestroyAttentionDescriptor(grxdnnAttentionDescriptor_t d);
+/* causal: 0 or 1. softmaxScale: finite and > 0 (1/sqrt(D) is the usual). */
+grxdnnStatus_t grxdnnSetAttentionDescriptor(grxdnnAttentionDescriptor_t d,
+                                            int causal, float softmaxScale);
+grxdnnStatus_t grxdnnGetAttentionDescriptor(grxdnnAttentionDescriptor_t d,
+                                            int* causal, float* softmaxScale);
+
+grxdnnStatus_t grxdnnAttentionForward(grxdnnHandle_t handle,
+                                      grxdnnAttentionDescriptor_t attnDesc,
+                                      grxdnnTensorDescriptor_t qDesc, const void* q,
+                                      grxdnnTensorDescriptor_t kDesc, const void* k,
+                                      grxdnnTensorDescriptor_t vDesc, const void* v,
+                                      grxdnnTensorDescriptor_t oDesc, void* o);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* GRXDNN_H */

@@ -1,0 +1,43 @@
+"""Shared helpers for the GPU parity tests (host-side only)."""
+import sys
+
+import numpy as np
+
+import grxcp_amd as g
+
+
+def say(msg: str) -> None:
+    """Name the case before a GPU step, flushed, so a crash log names it."""
+    sys.stdout.write(f"[case] {msg}\n")
+    sys.stdout.flush()
+
+
+def col_major(mat: np.ndarray, ld: int) -> np.ndarray:
+    rows, cols = mat.shape
+    buf = np.zeros(ld * cols, mat.dtype)
+    view = buf.reshape(cols, ld)
+    view[:, :rows] = mat.T
+    return buf
+
+
+def from_col_major(buf: np.ndarray, rows: int, cols: int, ld: int) -> np.ndarray:
+    return buf[: ld * cols].reshape(cols, ld)[:, :rows].T
+
+
+def window_mask(rows: int, cols: int, ld: int) -> np.ndarray:
+    """True inside the rows x cols window of a column-major ld buffer."""
+    m = np.zeros((cols, ld), bool)
+    m[:, :rows] = True
+    return m.reshape(-1)
+
+
+def normwise_rel_err(got: np.ndarray, ref: np.ndarray) -> float:
+    """max |got - ref| / max |ref|: the relative error the gates bound."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.max(np.abs(ref))
+    return float(np.max(np.abs(got - ref)) / (den if den > 0 else 1.0))
+
+
+def to_dev(a: np.ndarray) -> g.DeviceBuffer:
+    return g.DeviceBuffer.from_array(a)

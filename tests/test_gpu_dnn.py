@@ -1,0 +1,231 @@
+"""grxDNN RMSNorm / LayerNorm / attention on gfx950 against the CPU oracle.
+
+The reference has no grxDNN code to compare with (ref
+docs/designs/grxcp_roadmap.md:864-877), so the oracle follows the
+definitions (pinned in tests/test_oracle.py). Bounds, from the north star:
+norms within 1e-2 in bf16; attention within max relative error 1e-2 of the
+fp64 reference. Closed forms are checked exactly where the arithmetic is
+exact (LayerNorm of a constant row is beta; attention row 0 is V[0]).
+"""
+import numpy as np
+import pytest
+
+import grxcp_amd as g
+import oracle as O
+from helpers import normwise_rel_err, say, to_dev
+
+pytestmark = pytest.mark.gpu
+
+BF16, F16, F32 = g.GRX_R_16BF, g.GRX_R_16F, g.GRX_R_32F
+
+
+def enc(x: np.ndarray, t: int) -> np.ndarray:
+    if t == BF16:
+        return O.f32_to_bf16(x)
+    if t == F16:
+        return O.f32_to_half(x)
+    return np.ascontiguousarray(x, np.float32)
+
+
+def dec(b: np.ndarray, t: int) -> np.ndarray:
+    if t == BF16:
+        return O.bf16_to_f32(b)
+    if t == F16:
+        return O.half_to_f32(b)
+    return b
+
+
+def nptype(t):
+    return np.float32 if t == F32 else np.uint16
+
+
+def run_norm(dnn, layer, t, rows, hidden, seed, pitch=None, x=None, eps=1e-6):
+    r = np.random.default_rng(seed)
+    pitch = pitch or hidden
+    if x is None:
+        x = r.standard_normal((rows, hidden)).astype(np.float32)
+    gamma = (1 + 0.02 * r.standard_normal(hidden)).astype(np.float32)
+    beta = (0.02 * r.standard_normal(hidden)).astype(np.float32)
+    xe, ge, be = enc(x, t), enc(gamma, t), enc(beta, t)
+    xq, gq, bq = dec(xe, t), dec(ge, t), dec(be, t)       # what the kernel sees
+    xbuf = np.zeros((rows, pitch), nptype(t))
+    xbuf[:, :hidden] = xe
+    poison = np.full((rows, pitch), 0x7FC1 if t != F32 else np.float32(np.nan), nptype(t))
+    dx, dg, db, dy = to_dev(xbuf), to_dev(ge), to_dev(be), to_dev(poison)
+    xd = g.TensorDesc(t, [rows, hidden], [pitch, 1])
+    wd = g.TensorDesc(t, [hidden])
+    say(f"{'layernorm' if layer else 'rmsnorm'} t={t} rows={rows} hidden={hidden} pitch={pitch}")
+    if layer:
+        s = dnn.layernorm(xd, dx.p, wd, dg.p, db.p, eps, xd, dy.p)
+    else:
+        s = dnn.rmsnorm(xd, dx.p, wd, dg.p, eps, xd, dy.p)
+    assert s == g.SUCCESS, g.STATUS[s]
+    g.synchronize()
+    got = dy.download(nptype(t), rows * pitch).reshape(rows, pitch)
+    if pitch > hidden:  # the row padding is never written
+        pad = got[:, hidden:]
+        assert np.array_equal(pad.view(np.uint8), poison[:, hidden:].view(np.uint8))
+    yg = dec(np.ascontiguousarray(got[:, :hidden]), t)
+    ref = O.layernorm(xq, gq, bq, eps) if layer else O.rmsnorm(xq, gq, eps)
+    return yg, ref, bq
+
+
+SHAPES = [(1, 1), (3, 7), (5, 100), (64, 512), (33, 2048), (16, 4096), (8, 8192), (4, 16384),
+          (2, 16392), (2, 65536)]
+
+
+@pytest.mark.parametrize("layer", [False, True])
+@pytest.mark.parametrize("rows,hidden", SHAPES)
+def test_norm_bf16_vs_oracle(dnn, layer, rows, hidden):
+    y, ref, _ = run_norm(dnn, layer, BF16, rows, hidden, seed=rows + hidden)
+    if hidden == 1 and layer:
+        # a one-element row normalises to beta exactly
+        assert np.array_equal(y, O.bf16_to_f32(O.f32_to_bf16(ref)))
+    assert np.max(np.abs(y - ref)) <= 1e-2 * max(1.0, np.max(np.abs(ref)))
+
+
+@pytest.mark.parametrize("t", [F16, F32])
+@pytest.mark.parametrize("layer", [False, True])
+def test_norm_other_types(dnn, t, layer):
+    y, ref, _ = run_norm(dnn, layer, t, 24, 1024, seed=5)
+    tol = 1e-5 if t == F32 else 2e-3
+    assert np.max(np.abs(y - ref)) <= tol * max(1.0, np.max(np.abs(ref)))
+
+
+@pytest.mark.parametrize("layer", [False, True])
+def test_norm_padded_rows(dnn, layer):
+    y, ref, _ = run_norm(dnn, layer, BF16, 40, 1000, seed=9, pitch=1008)
+    assert np.max(np.abs(y - ref)) <= 1e-2
+
+
+def test_layernorm_constant_rows_give_beta_exactly(dnn):
+    rows, hidden = 6, 8192
+    x = np.repeat(np.array([1.5, -2.25, 0.0, 3.0, 1e-3, -7.0], np.float32)[:, None], hidden, 1)
+    y, _, bq = run_norm(dnn, True, BF16, rows, hidden, seed=2, x=x)
+    assert np.array_equal(y, np.tile(O.bf16_to_f32(O.f32_to_bf16(bq)), (rows, 1)))
+
+
+def test_config4_full_size_sampled(dnn):
+    """BASELINE config 4 at full size (16384 x 8192 bf16): every row computed on
+    the GPU, 64 sampled rows checked against the oracle within 1e-2."""
+    from grxcp_amd import synth
+    rows, hidden = 16384, 8192
+    xb = synth.normal_bf16(rows * hidden, 41).reshape(rows, hidden)
+    gb = synth.normal_bf16(hidden, 42, 1.0, 0.02)
+    bb = synth.normal_bf16(hidden, 43, 0.0, 0.02)
+    dx, dg, db, dy = to_dev(xb), to_dev(gb), to_dev(bb), g.DeviceBuffer(rows * hidden * 2)
+    xd, wd = g.TensorDesc(BF16, [rows, hidden]), g.TensorDesc(BF16, [hidden])
+    pick = np.random.default_rng(0).choice(rows, 64, replace=False)
+    for layer in (False, True):
+        say(f"config4 {'layernorm' if layer else 'rmsnorm'} full size")
+        s = (dnn.layernorm(xd, dx.p, wd, dg.p, db.p, 1e-6, xd, dy.p) if layer
+             else dnn.rmsnorm(xd, dx.p, wd, dg.p, 1e-6, xd, dy.p))
+        assert s == 0
+        g.synchronize()
+        y = dy.download(np.uint16, rows * hidden).reshape(rows, hidden)
+        xs = O.bf16_to_f32(xb[pick])
+        gf, bf = O.bf16_to_f32(gb), O.bf16_to_f32(bb)
+        ref = O.layernorm(xs, gf, bf, 1e-6) if layer else O.rmsnorm(xs, gf, 1e-6)
+        assert np.max(np.abs(O.bf16_to_f32(y[pick]) - ref)) <= 1e-2 * np.max(np.abs(ref))
+        assert np.isfinite(O.bf16_to_f32(y)).all()
+
+
+# ---- attention -----------------------------------------------------------------
+
+def run_attention(dnn, t, B, H, S, D, causal, seed, q=None, k=None, v=None):
+    r = np.random.default_rng(seed)
+    shp = (B, H, S, D)
+    q = r.standard_normal(shp).astype(np.float32) if q is None else q
+    k = r.standard_normal(shp).astype(np.float32) if k is None else k
+    v = r.standard_normal(shp).astype(np.float32) if v is None else v
+    qe, ke, ve = enc(q, t), enc(k, t), enc(v, t)
+    dq, dk, dv = to_dev(qe), to_dev(ke), to_dev(ve)
+    do = g.DeviceBuffer(qe.nbytes)
+    desc = g.TensorDesc(t, list(shp))
+    ad = g.AttnDesc(causal, D ** -0.5)
+    say(f"attention t={t} B={B} H={H} S={S} D={D} causal={causal}")
+    s = dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p)
+    assert s == g.SUCCESS, g.STATUS[s]
+    g.synchronize()
+    o = dec(do.download(np.uint16, qe.size), t).reshape(shp)
+    return o, dec(qe, t).reshape(shp), dec(ke, t).reshape(shp), dec(ve, t).reshape(shp)
+
+
+@pytest.mark.parametrize("t", [BF16, F16])
+@pytest.mark.parametrize("S,D,causal", [(128, 128, True), (256, 128, True), (256, 128, False),
+                                        (200, 128, True), (1, 128, True), (130, 64, True),
+                                        (333, 64, False), (64, 128, False)])
+def test_attention_vs_oracle(dnn, t, S, D, causal):
+    B, H = 2, 3
+    o, q, k, v = run_attention(dnn, t, B, H, S, D, causal, seed=S + D)
+    for b in range(B):
+        for h in range(H):
+            ref = O.attention_head(q[b, h], k[b, h], v[b, h], causal, D ** -0.5)
+            assert normwise_rel_err(o[b, h], ref) <= 1e-2, (b, h)
+
+
+def test_attention_closed_forms(dnn):
+    B, H, S, D = 1, 2, 256, 128
+    r = np.random.default_rng(1)
+    v = r.standard_normal((B, H, S, D)).astype(np.float32)
+    o, _, _, vq = run_attention(dnn, BF16, B, H, S, D, True, seed=3, v=v)
+    # row 0 attends to key 0 only: O[0] == V[0] exactly
+    assert np.array_equal(o[:, :, 0], vq[:, :, 0])
+    # Q = 0: uniform weights over the causal prefix -> running mean of V
+    o0, _, _, vq0 = run_attention(dnn, BF16, B, H, S, D, True, seed=4, q=np.zeros((B, H, S, D), np.float32),
+                                  v=v)
+    want = np.cumsum(vq0.astype(np.float64), 2) / np.arange(1, S + 1)[None, None, :, None]
+    assert normwise_rel_err(o0, want) <= 1e-2
+    # V constant along keys -> O = V
+    vc = np.broadcast_to(r.standard_normal((B, H, 1, D)).astype(np.float32), (B, H, S, D)).copy()
+    oc, _, _, vqc = run_attention(dnn, BF16, B, H, S, D, True, seed=5, v=vc)
+    assert normwise_rel_err(oc, vqc) <= 1e-2
+
+
+def test_attention_strided_layout(dnn):
+    """[B, S, H, D] storage described by strides (heads interleaved)."""
+    B, H, S, D = 2, 4, 192, 128
+    r = np.random.default_rng(11)
+    x = [r.standard_normal((B, S, H, D)).astype(np.float32) for _ in range(3)]
+    enc3 = [O.f32_to_bf16(a) for a in x]
+    dev = [to_dev(a) for a in enc3]
+    do = g.DeviceBuffer(enc3[0].nbytes)
+    strides = [S * H * D, D, H * D, 1]
+    desc = g.TensorDesc(BF16, [B, H, S, D], strides)
+    ad = g.AttnDesc(True, D ** -0.5)
+    say("attention strided [B,S,H,D]")
+    assert dnn.attention(ad, desc, dev[0].p, desc, dev[1].p, desc, dev[2].p, desc, do.p) == 0
+    g.synchronize()
+    o = O.bf16_to_f32(do.download(np.uint16, enc3[0].size)).reshape(B, S, H, D)
+    qf, kf, vf = (O.bf16_to_f32(a).reshape(B, S, H, D) for a in enc3)
+    for b in range(B):
+        for h in range(H):
+            ref = O.attention_head(qf[b, :, h], kf[b, :, h], vf[b, :, h], True, D ** -0.5)
+            assert normwise_rel_err(o[b, :, h], ref) <= 1e-2
+
+
+def test_config5_full_size_sampled(dnn):
+    """BASELINE config 5 at full size (B4 H32 S4096 D128 bf16, causal): all
+    heads computed on the GPU; sampled heads and query rows (including the
+    first and last of tiles and the sequence) checked against the oracle."""
+    from grxcp_amd import synth
+    B, H, S, D = 4, 32, 4096, 128
+    n = B * H * S * D
+    qb, kb, vb = (synth.normal_bf16(n, s) for s in (51, 52, 53))
+    dq, dk, dv, do = to_dev(qb), to_dev(kb), to_dev(vb), g.DeviceBuffer(n * 2)
+    desc = g.TensorDesc(BF16, [B, H, S, D])
+    ad = g.AttnDesc(True, D ** -0.5)
+    say("config5 attention full size")
+    assert dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p) == 0
+    g.synchronize()
+    o = do.download(np.uint16, n).reshape(B, H, S, D)
+    rows = [0, 1, 63, 64, 127, 128, 129, 1000, 2047, 2048, 4094, 4095]
+    for (b, h) in [(0, 0), (1, 17), (3, 31)]:
+        q = O.bf16_to_f32(qb.reshape(B, H, S, D)[b, h])
+        k = O.bf16_to_f32(kb.reshape(B, H, S, D)[b, h])
+        v = O.bf16_to_f32(vb.reshape(B, H, S, D)[b, h])
+        for r0 in rows:
+            ref = O.attention_head(q, k, v, True, D ** -0.5, r0, r0 + 1)[r0]
+            got = O.bf16_to_f32(o[b, h, r0])
+            assert normwise_rel_err(got, ref) <= 1e-2, (b, h, r0)
+    assert np.isfinite(O.bf16_to_f32(o)).all()

@@ -1,0 +1,299 @@
+"""grxblasGemmEx / grxblasGemmExDequant on gfx950 against the CPU oracle.
+
+Mirrors the reference's GemmEx gate (ref tests/libs/test_grxblas_ex.cpp):
+exact-by-construction inputs (multiples of 0.5 in [-4, 4], exact in fp16 and
+bf16, products and sums exact in fp32), so the comparison is BIT-EXACT over
+the ENTIRE padded C buffer -- inside the window and in the padding -- for
+ragged shapes and all four transposes, with the tile shape queried from the
+library. int8 is integer and exact. Random-normal cases (the BASELINE config
+distributions) use the north-star bound: max relative error <= 1e-2 vs an
+fp32/fp64 reference.
+"""
+import numpy as np
+import pytest
+
+import grxcp_amd as g
+import oracle as O
+from helpers import col_major, from_col_major, normwise_rel_err, say, to_dev, window_mask
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, F32, I8, I32 = g.GRX_R_16F, g.GRX_R_16BF, g.GRX_R_32F, g.GRX_R_8I, g.GRX_R_32I
+
+
+def narrow(vals: np.ndarray, t: int) -> np.ndarray:
+    return O.f32_to_half(vals) if t == F16 else O.f32_to_bf16(vals)
+
+
+def widen(bits: np.ndarray, t: int) -> np.ndarray:
+    return O.half_to_f32(bits) if t == F16 else O.bf16_to_f32(bits)
+
+
+def float_case(blas, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad=None, seed=99):
+    """The reference's run_case (ref test_grxblas_ex.cpp:65-149), for any
+    fp16/bf16 input and fp32/fp16/bf16 output. `pad` widens lda/ldb, `cpad`
+    (default: pad) widens ldc. Returns (#wrong, #stray)."""
+    kk = k if k else 1
+    a_rows, a_cols = (kk, m) if ta else (m, kk)
+    b_rows, b_cols = (n, kk) if tb else (kk, n)
+    lda, ldb, ldc = a_rows + pad, b_rows + pad, m + (pad if cpad is None else cpad)
+    st = O.HalvesStream(seed)
+    A = st.take(lda * a_cols)
+    B = st.take(ldb * b_cols)
+    C = st.take(ldc * n) * 2.0
+    hA, hB = narrow(A, in_t), narrow(B, in_t)
+    assert np.array_equal(widen(hA, in_t), A) and np.array_equal(widen(hB, in_t), B)
+    if out_t == F32:
+        c_host = C
+        expected = O.gemm_f32acc(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
+    else:
+        c_host = narrow(C, out_t)
+        c_in = widen(c_host, out_t)
+        expected = narrow(O.gemm_f32acc(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, c_in, ldc), out_t)
+        # the padding must come back as uploaded
+        inside = window_mask(m, n, ldc)
+        expected = np.where(inside, expected, c_host)
+    dA, dB, dC = to_dev(hA), to_dev(hB), to_dev(c_host)
+    say(f"gemm_ex in={in_t} out={out_t} ta={ta} tb={tb} {m}x{n}x{k} a={alpha} b={beta} pad={pad}")
+    s = blas.gemm_ex(ta, tb, m, n, k, alpha, dA.p, in_t, lda, dB.p, in_t, ldb, beta, dC.p, out_t, ldc)
+    assert s == g.SUCCESS, g.STATUS[s]
+    g.synchronize()
+    got = dC.download(c_host.dtype, c_host.size)
+    inside = window_mask(m, n, ldc)
+    diff = got.view(np.uint32 if got.itemsize == 4 else np.uint16) != \
+        expected.astype(c_host.dtype).view(np.uint32 if got.itemsize == 4 else np.uint16)
+    return int(np.sum(diff & inside)), int(np.sum(diff & ~inside))
+
+
+def gate_cases(tm, tn, tk):
+    """The reference's case list (ref test_grxblas_ex.cpp:207-242)."""
+    cases = [
+        (0, 0, tm, tn, tk, 1.0, 0.0, 0), (0, 0, tm * 2, tn * 2, tk * 2, 1.0, 0.0, 0),
+        (0, 0, 16, 16, 16, 1.0, 0.0, 0), (0, 0, 5, 3, 7, 1.0, 0.0, 0),
+        (0, 0, 17, 9, 13, 1.0, 0.0, 0), (0, 0, 1, 1, 1, 1.0, 0.0, 0),
+        (0, 0, 12, 6, 10, 2.5, -1.5, 0), (0, 0, 12, 6, 10, 1.0, 0.0, 3),
+        (0, 0, 6, 5, 0, 1.0, 2.0, 0),
+    ]
+    for which in range(3):
+        ta, tb = int(which != 1), int(which != 0)
+        cases += [(ta, tb, tm, tn, tk, 1.0, 0.0, 0), (ta, tb, tm * 2, tn * 2, tk * 2, 1.0, 0.0, 0),
+                  (ta, tb, 5, 3, 7, 1.0, 0.0, 0), (ta, tb, 17, 9, 13, 1.0, 0.0, 0),
+                  (ta, tb, 12, 6, 10, 2.5, -1.5, 3)]
+    return cases
+
+
+def test_tensor_tile_and_types(blas):
+    import ctypes
+    m, n, k, t = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_uint()
+    assert blas.L.grxblasGetTensorTile(blas.h, ctypes.byref(m), ctypes.byref(n), ctypes.byref(k)) == 0
+    assert (m.value, n.value, k.value) == (32, 32, 16)
+    assert blas.L.grxblasGetTensorTypes(blas.h, ctypes.byref(t)) == 0
+    assert t.value & g.TENSOR_FP16 and t.value & g.TENSOR_BF16 and t.value & g.TENSOR_INT8
+    p = ctypes.c_char_p()
+    assert blas.L.grxblasGetLoadedKernelPath(blas.h, ctypes.byref(p)) == 0
+    assert p.value and p.value.decode().endswith("libgrxblas.so")
+
+
+@pytest.mark.parametrize("in_t,out_t", [(F16, F32), (BF16, F32), (BF16, BF16), (F16, F16)])
+def test_reference_gemm_ex_gate(blas, in_t, out_t):
+    bad = []
+    for case in gate_cases(32, 32, 16):
+        ta, tb, m, n, k, a, b, pad = case
+        wrong, stray = float_case(blas, in_t, out_t, ta, tb, m, n, k, a, b, pad)
+        if wrong or stray:
+            bad.append((case, wrong, stray))
+    assert not bad, bad
+
+
+# Fast (TN, K-contiguous) path: still exact-by-construction, at sizes and
+# alignments that route to the 256x256 MFMA kernel, with ragged m/n and a k
+# that does not fill the last 128-byte stage.
+# (m, n, k, pad, cpad): lda = k + pad and ldc = m + cpad are multiples of 8
+# wherever the fast path is meant to run.
+FAST_SHAPES = [
+    (256, 256, 64, 0, 0), (512, 256, 128, 0, 0), (300, 200, 200, 8, 4), (1, 1, 8, 0, 0),
+    (257, 513, 1024, 8, 7), (1024, 768, 2048, 0, 0),
+]
+
+
+@pytest.mark.parametrize("in_t,out_t", [(BF16, F32), (BF16, BF16), (F16, F32)])
+@pytest.mark.parametrize("m,n,k,pad,cpad", FAST_SHAPES)
+def test_fast_path_exact(blas, in_t, out_t, m, n, k, pad, cpad):
+    wrong, stray = float_case(blas, in_t, out_t, 1, 0, m, n, k, 1.0, 0.0, pad, cpad)
+    assert (wrong, stray) == (0, 0)
+
+
+def test_fast_path_alpha_beta(blas):
+    assert float_case(blas, BF16, F32, 1, 0, 384, 320, 256, 2.5, -1.5, 8) == (0, 0)
+    assert float_case(blas, BF16, BF16, 1, 0, 384, 320, 256, 2.5, -1.5, 8) == (0, 0)
+    assert float_case(blas, F16, F16, 1, 0, 384, 320, 256, 2.5, -1.5, 8) == (0, 0)
+
+
+def int8_case(blas, ta, tb, m, n, k, alpha, beta, pad, fill="ref", seed=0, cpad=None):
+    """The reference's int8_case (ref test_grxblas_ex.cpp:254-322)."""
+    kk = k if k else 1
+    a_rows, a_cols = (kk, m) if ta else (m, kk)
+    b_rows, b_cols = (n, kk) if tb else (kk, n)
+    lda, ldb, ldc = a_rows + pad, b_rows + pad, m + (pad if cpad is None else cpad)
+    if fill == "ref":
+        ia = np.arange(lda * a_cols, dtype=np.int64)
+        A = ((ia * 7 % 15) - 7).astype(np.int8)
+        B = ((np.arange(ldb * b_cols, dtype=np.int64) * 5 % 13) - 6).astype(np.int8)
+        C = ((np.arange(ldc * n, dtype=np.int64) * 3 % 41) - 20).astype(np.int32)
+    else:
+        r = np.random.default_rng(seed)
+        A = r.integers(-127, 128, lda * a_cols).astype(np.int8)
+        B = r.integers(-127, 128, ldb * b_cols).astype(np.int8)
+        C = r.integers(-1000, 1000, ldc * n).astype(np.int32)
+    want = O.igemm(ta, tb, m, n, k, int(alpha), A, lda, B, ldb, int(beta), C, ldc)
+    dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
+    say(f"igemm ta={ta} tb={tb} {m}x{n}x{k} a={alpha} b={beta} pad={pad}")
+    s = blas.gemm_ex(ta, tb, m, n, k, alpha, dA.p, I8, lda, dB.p, I8, ldb, beta, dC.p, I32, ldc)
+    assert s == g.SUCCESS, g.STATUS[s]
+    g.synchronize()
+    got = dC.download(np.int32, C.size)
+    return int(np.sum(got != want))
+
+
+def test_reference_int8_gate(blas):
+    # ref test_grxblas_ex.cpp:324-331
+    cases = [(0, 0, 32, 32, 16, 1, 0, 0), (0, 0, 16, 16, 32, 1, 0, 0), (0, 0, 5, 3, 7, 1, 0, 0),
+             (0, 0, 17, 9, 29, 2, -1, 3), (1, 0, 13, 7, 19, 1, 0, 0), (0, 1, 13, 7, 19, 1, 0, 0),
+             (1, 1, 13, 7, 19, 1, 1, 0)]
+    bad = [(c, int8_case(blas, *c)) for c in cases]
+    assert all(n == 0 for _, n in bad), bad
+
+
+@pytest.mark.parametrize("m,n,k,pad,cpad", [(256, 256, 128, 0, 0), (300, 200, 272, 16, 4),
+                                            (512, 768, 4096, 0, 0), (1, 2, 16, 0, 0),
+                                            (1000, 1000, 1040, 0, 0)])
+def test_int8_fast_path_exact(blas, m, n, k, pad, cpad):
+    assert int8_case(blas, 1, 0, m, n, k, 1, 0, pad, fill="rand", seed=m + n + k, cpad=cpad) == 0
+    assert int8_case(blas, 1, 0, m, n, k, 3, -2, pad, fill="rand", seed=m + n + k + 1, cpad=cpad) == 0
+
+
+def test_int8_refusals(blas):
+    d = g.DeviceBuffer(4096)
+    # ref test_grxblas_ex.cpp:334-340
+    assert blas.gemm_ex(0, 0, 8, 4, 16, 2.5, d.p, I8, 8, d.p, I8, 16, 0.0, d.p, I32, 8) == g.INVALID_VALUE
+    assert blas.gemm_ex(0, 0, 8, 4, 16, 1.0, d.p, I8, 8, d.p, I8, 16, 0.5, d.p, I32, 8) == g.INVALID_VALUE
+    # ref test_grxblas_ex.cpp:345-371
+    assert blas.gemm_ex(1, 0, 4, 4, 8, 1.0, d.p, F16, 4, d.p, F16, 8, 0.0, d.p, F32, 4) == g.INVALID_VALUE
+    assert blas.gemm_ex(0, 0, 8, 4, 8, 1.0, d.p, F32, 8, d.p, F16, 8, 0.0, d.p, F32, 8) == g.NOT_SUPPORTED
+    assert blas.gemm_ex(0, 0, 8, 4, 8, 1.0, d.p, F16, 2, d.p, F16, 8, 0.0, d.p, F32, 8) == g.INVALID_VALUE
+    assert blas.gemm_ex(0, 0, 8, 4, 8, 1.0, d.p, F16, 8, d.p, BF16, 8, 0.0, d.p, F32, 8) == g.NOT_SUPPORTED
+    assert blas.gemm_ex(0, 0, 8, 4, 8, 1.0, d.p, I8, 8, d.p, I8, 8, 0.0, d.p, F32, 8) == g.NOT_SUPPORTED
+    assert blas.gemm_ex_dequant(0, 0, 8, 4, 8, d.p, I8, 8, d.p, I8, 8, None, d.p, BF16, 8) == g.INVALID_VALUE
+    assert blas.gemm_ex_dequant(0, 0, 8, 4, 8, d.p, I8, 8, d.p, I8, 8, d.p, d.p, F32, 8) == g.NOT_SUPPORTED
+
+
+def dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed):
+    kk = k if k else 1
+    a_rows, a_cols = (kk, m) if ta else (m, kk)
+    b_rows, b_cols = (n, kk) if tb else (kk, n)
+    lda, ldb, ldc = a_rows + pad, b_rows + pad, m + cpad
+    r = np.random.default_rng(seed)
+    A = r.integers(-127, 128, lda * a_cols).astype(np.int8)
+    B = r.integers(-127, 128, ldb * b_cols).astype(np.int8)
+    scale = r.uniform(0.001, 0.01, n).astype(np.float32)
+    acc = O.igemm(ta, tb, m, n, k, 1, A, lda, B, ldb, 0, np.zeros(m * n, np.int32), m)
+    want = O.dequant(m, n, acc, m, scale, ldc)
+    poison = np.full(ldc * n, 0x7FC1, np.uint16)
+    dA, dB, dS, dC = to_dev(A), to_dev(B), to_dev(scale), to_dev(poison)
+    say(f"dequant ta={ta} tb={tb} {m}x{n}x{k} pad={pad}")
+    s = blas.gemm_ex_dequant(ta, tb, m, n, k, dA.p, I8, lda, dB.p, I8, ldb, dS.p, dC.p, BF16, ldc)
+    assert s == g.SUCCESS, g.STATUS[s]
+    g.synchronize()
+    got = dC.download(np.uint16, ldc * n)
+    inside = window_mask(m, n, ldc)
+    return int(np.sum((got != want) & inside)), int(np.sum((got != poison) & ~inside))
+
+
+@pytest.mark.parametrize("ta,tb,m,n,k,pad,cpad", [
+    (1, 0, 256, 256, 256, 0, 0), (1, 0, 300, 260, 528, 16, 4), (0, 0, 37, 29, 45, 3, 3),
+    (1, 1, 33, 65, 77, 0, 0), (0, 1, 64, 64, 64, 0, 0), (1, 0, 5, 3, 0, 0, 0),
+])
+def test_dequant_bit_exact(blas, ta, tb, m, n, k, pad, cpad):
+    assert dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed=m * 7 + n + k) == (0, 0)
+
+
+def test_bf16_random_normal_tolerance(blas):
+    """Config-2 distribution (N(0,1) bf16, TN, bf16 out) at 1024^3 and a
+    ragged shape: max relative error vs a float64 reference <= 1e-2."""
+    for (m, n, k) in [(1024, 1024, 1024), (777, 555, 1000)]:
+        r = np.random.default_rng(m)
+        A = O.f32_to_bf16(r.standard_normal(m * k).astype(np.float32))   # op(A) row-major m x k
+        B = O.f32_to_bf16(r.standard_normal(n * k).astype(np.float32))   # col-major k x n
+        dA, dB, dC = to_dev(A), to_dev(B), g.DeviceBuffer(m * n * 2)
+        say(f"bf16 normal {m}x{n}x{k}")
+        assert blas.gemm_ex(1, 0, m, n, k, 1.0, dA.p, BF16, k, dB.p, BF16, k, 0.0, dC.p, BF16, m) == 0
+        g.synchronize()
+        got = O.bf16_to_f32(dC.download(np.uint16, m * n))
+        ref = O.sgemm(1, 0, m, n, k, 1.0, O.bf16_to_f32(A), k, O.bf16_to_f32(B), k, 0.0,
+                      np.zeros(m * n, np.float32), m)
+        assert normwise_rel_err(got, ref) <= 1e-2
+
+
+def test_config2_bf16_8192_sampled(blas):
+    """BASELINE config 2 at full size: bf16 8192^3, TN (row-major A x
+    column-major B), bf16 C. Sampled rows x columns against the fp64 oracle on
+    the same bf16 inputs, max relative error <= 1e-2; every output finite."""
+    from grxcp_amd import synth
+    M = N = K = 8192
+    A = synth.normal_bf16(M * K, 21)   # op(A): row-major M x K  (grxBLAS: transa=T, lda=K)
+    B = synth.normal_bf16(N * K, 22)   # column-major K x N      (transb=N, ldb=K)
+    dA, dB, dC = to_dev(A), to_dev(B), g.DeviceBuffer(M * N * 2)
+    say("config2 bf16 8192^3")
+    assert blas.gemm_ex(1, 0, M, N, K, 1.0, dA.p, BF16, K, dB.p, BF16, K, 0.0, dC.p, BF16, M) == 0
+    g.synchronize()
+    C = O.bf16_to_f32(dC.download(np.uint16, M * N)).reshape(N, M)   # C[j, i] (column-major)
+    assert np.isfinite(C).all()
+    r = np.random.default_rng(0)
+    rows = np.sort(np.concatenate([[0, 255, 256, M - 1], r.choice(M, 12, replace=False)]))
+    cols = np.sort(np.concatenate([[0, 255, 256, N - 1], r.choice(N, 124, replace=False)]))
+    a = O.bf16_to_f32(A.reshape(M, K)[rows])          # len(rows) x K
+    b = O.bf16_to_f32(B.reshape(N, K)[cols])          # len(cols) x K
+    m, n = len(rows), len(cols)
+    ref = O.sgemm(1, 0, m, n, K, 1.0, a.reshape(-1), K, b.reshape(-1), K, 0.0,
+                  np.zeros(m * n, np.float32), m).reshape(n, m)
+    got = C[np.ix_(cols, rows)]
+    assert normwise_rel_err(got, ref) <= 1e-2
+
+
+def test_config3_int8_full_size(blas):
+    """BASELINE config 3 at full size: M=4096 tokens, K=8192, N=28672; int8
+    U[-127,127]. int32 C bit-exact on sampled rows x columns against the
+    oracle, plus the whole-matrix checksum identity
+    sum_ij C = sum_l (sum_i A[i,l]) (sum_j B[l,j]); then the per-channel
+    dequant to bf16 bit-exact on the same samples."""
+    from grxcp_amd import synth
+    M, K, N = 4096, 8192, 28672
+    A = synth.uniform_int8(M * K, 31)   # row-major M x K  (transa=T, lda=K)
+    B = synth.uniform_int8(N * K, 32)   # column-major K x N (transb=N, ldb=K)
+    scale = synth.uniform_f32(N, 33, 0.001, 0.01)
+    dA, dB, dC = to_dev(A), to_dev(B), g.DeviceBuffer(M * N * 4)
+    say("config3 int8 int32 full size")
+    assert blas.gemm_ex(1, 0, M, N, K, 1.0, dA.p, I8, K, dB.p, I8, K, 0.0, dC.p, I32, M) == 0
+    g.synchronize()
+    C = dC.download(np.int32, M * N).reshape(N, M)
+    colsum_a = A.reshape(M, K).sum(0, dtype=np.int64)
+    rowsum_b = B.reshape(N, K).sum(0, dtype=np.int64)
+    assert int(C.sum(dtype=np.int64)) == int(np.dot(colsum_a, rowsum_b))
+    r = np.random.default_rng(1)
+    rows = np.sort(np.concatenate([[0, 255, 256, M - 1], r.choice(M, 12, replace=False)]))
+    cols = np.sort(np.concatenate([[0, 255, 256, N - 1], r.choice(N, 252, replace=False)]))
+    m, n = len(rows), len(cols)
+    a = np.ascontiguousarray(A.reshape(M, K)[rows])
+    b = np.ascontiguousarray(B.reshape(N, K)[cols])
+    want = O.igemm(1, 0, m, n, K, 1, a.reshape(-1), K, b.reshape(-1), K, 0, np.zeros(m * n, np.int32),
+                   m).reshape(n, m)
+    assert np.array_equal(C[np.ix_(cols, rows)], want)
+    del C
+    dC.close()
+    dS, dY = to_dev(scale), g.DeviceBuffer(M * N * 2)
+    say("config3 int8 dequant full size")
+    assert blas.gemm_ex_dequant(1, 0, M, N, K, dA.p, I8, K, dB.p, I8, K, dS.p, dY.p, BF16, M) == 0
+    g.synchronize()
+    Y = dY.download(np.uint16, M * N).reshape(N, M)
+    yw = O.dequant(m, n, want.reshape(-1), m, scale[cols], m).reshape(n, m)
+    assert np.array_equal(Y[np.ix_(cols, rows)], yw)
