@@ -236,62 +236,59 @@ constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
 
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
 template <class Op, MmaOut OUT>
 __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
-  __shared__ __attribute__((aligned(16))) i32x4 lds[2][2][kFastTile * kChunks];
+  // [stage][A | B][row * 8 + physical chunk], 16 bytes per entry: 128 KB.
+  __shared__ __attribute__((aligned(1024))) i32x4 lds[2][2][kFastTile * kChunks];
 
   const uint64_t t0 = p.probe ? cycle_now() : 0;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   int tm, tn;
   map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
   const int row0 = tm * kFastTile;
   const int col0 = tn * kFastTile;
 
-  const int64_t lda_b = p.lda * Op::kElemBytes;
-  const int64_t ldb_b = p.ldb * Op::kElemBytes;
+  const int lda_b = (int)(p.lda * Op::kElemBytes);
+  const int ldb_b = (int)(p.ldb * Op::kElemBytes);
   const int kbytes = p.k * Op::kElemBytes;
   const int ktiles = (kbytes + kFastKBytes - 1) / kFastKBytes;
 
   // Buffer descriptors start at this tile's first row; the record count ends
-  // at row m (n), so rows past the matrix read as zero without a branch.
+  // at row m (n), so rows past the matrix read as zero without a branch, and
+  // an offset of 2^31 (always past the end) reads zero for a masked k chunk.
   const int rows_a = min(kFastTile, p.m - row0);
   const int rows_b = min(kFastTile, p.n - col0);
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.a + (int64_t)row0 * lda_b), (short)0,
-      (int)((int64_t)(rows_a - 1) * lda_b + kbytes), kRsrcWord3);
+      (void*)(p.a + (int64_t)row0 * lda_b), (short)0, (rows_a - 1) * lda_b + kbytes, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.b + (int64_t)col0 * ldb_b), (short)0,
-      (int)((int64_t)(rows_b - 1) * ldb_b + kbytes), kRsrcWord3);
+      (void*)(p.b + (int64_t)col0 * ldb_b), (short)0, (rows_b - 1) * ldb_b + kbytes, kRsrcWord3);
+  constexpr uint32_t kOff = 0x80000000u;
 
-  // Loader: thread t moves 16-byte chunk (t & 7) of rows (t >> 3) + 32*i.
-  const int lrow = tid >> 3;
-  const int lch = tid & 7;
-  const uint32_t voff_a = (uint32_t)(lrow * lda_b + lch * 16);
-  const uint32_t voff_b = (uint32_t)(lrow * ldb_b + lch * 16);
-  const uint32_t step_a = (uint32_t)(32 * lda_b);
-  const uint32_t step_b = (uint32_t)(32 * ldb_b);
-
-  i32x4 ga[8], gb[8];
-  auto load_stage = [&](int kt) {
+  // Direct-to-LDS staging (buffer_load_dwordx4 ... lds): instruction i of
+  // wave w fills the 1 KB block of rows 8*(4i+w) .. +7, lane L landing in
+  // row +L/8 at physical chunk L%8. The swizzle is applied on the global
+  // side: that lane fetches logical chunk (L%8) ^ swz(row). No VGPRs hold
+  // the tile, and nothing waits for the data until the stage's barrier.
+  const int lr = lane >> 3;
+  const int pc = lane & 7;
+  auto issue_stage = [&](int kt, int st) {
     const int kb = kt * kFastKBytes;
-    const bool kvalid = kb + lch * 16 < kbytes;
+    const bool live = kt < ktiles;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      ga[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, voff_a + i * step_a + kb, 0, 0);
-      gb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, voff_b + i * step_b + kb, 0, 0);
-      if (!kvalid) { ga[i] = i32x4{0, 0, 0, 0}; gb[i] = i32x4{0, 0, 0, 0}; }
-    }
-  };
-  auto store_stage = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = lrow + 32 * i;
-      const int slot = row * kChunks + (lch ^ swz(row));
-      lds[st][0][slot] = ga[i];
-      lds[st][1][slot] = gb[i];
+      const int blk = 4 * i + wave;               // 8-row block index, 0..31
+      const int row = 8 * blk + lr;
+      const int c = pc ^ lr ^ (blk & 7);          // == pc ^ swz(row)
+      const bool ok = live && kb + 16 * c < kbytes;
+      const uint32_t va = ok ? (uint32_t)(row * lda_b + 16 * c + kb) : kOff;
+      const uint32_t vb = ok ? (uint32_t)(row * ldb_b + 16 * c + kb) : kOff;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&lds[st][0][blk * 64], 16, va, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&lds[st][1][blk * 64], 16, vb, 0, 0, 0);
     }
   };
 
@@ -309,36 +306,74 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
   const int r32 = lane & 31;
   const int hh = lane >> 5;
 
-  if (ktiles > 0) {
-    load_stage(0);
-    store_stage(0);
-  }
-  __syncthreads();
+  // Fragment reads: A rows wm*128 + 32t + r32, B rows wn*128 + 32t + r32,
+  // 16 bytes at logical chunk 2*ks + hh. Two register sets: the reads for
+  // k-step ks+1 are in flight while the 16 MFMAs of k-step ks run.
+  i32x4 fa[2][4], fb[2][4];
+  auto read_frags = [&](int st, int ks, int buf) {
+    const int kc = 2 * ks + hh;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int ar = wm * 128 + t * 32 + r32;
+      const int br = wn * 128 + t * 32 + r32;
+      fa[buf][t] = lds[st][0][ar * kChunks + (kc ^ swz(ar))];
+      fb[buf][t] = lds[st][1][br * kChunks + (kc ^ swz(br))];
+    }
+  };
+  auto mma_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = Op::mma(fa[buf][i], fb[buf][j], acc[i][j]);
+  };
+  // Interleave: 8 LDS reads (next fragments), each behind one MFMA, then
+  // the remaining 8 MFMAs.
+  auto interleave_reads = [&]() {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  };
 
+  issue_stage(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  read_frags(0, 0, 0);
+
+  // Per stage: the DMA for stage kt+1 goes out first; k-steps 0..2 run with
+  // the next k-step's fragments loading behind them; then one barrier makes
+  // stage kt+1 visible (and retires every wave's reads of stage kt), and
+  // k-step 3 runs while the next stage's first fragments load.
   for (int kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
-    const bool more = kt + 1 < ktiles;
-    if (more) load_stage(kt + 1);
-
+    issue_stage(kt + 1, cur ^ 1);
+    read_frags(cur, 1, 1);
+    mma_step(0);
+    // k-step 0 also carries the 16 DMA issues of the next stage
 #pragma unroll
-    for (int ks = 0; ks < kChunks / 2; ++ks) {
-      const int kc = 2 * ks + hh;
-      i32x4 fa[4], fb[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int ra_row = wm * 128 + t * 32 + r32;
-        const int rb_row = wn * 128 + t * 32 + r32;
-        fa[t] = lds[cur][0][ra_row * kChunks + (kc ^ swz(ra_row))];
-        fb[t] = lds[cur][1][rb_row * kChunks + (kc ^ swz(rb_row))];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = Op::mma(fa[i], fb[j], acc[i][j]);
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // 2 VMEM (DMA) issues
     }
-
-    if (more) store_stage(cur ^ 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(cur, 2, 0);
+    mma_step(1);
+    interleave_reads();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(cur, 3, 1);
+    mma_step(0);
+    interleave_reads();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    read_frags(cur ^ 1, 0, 0);
+    mma_step(1);
+    interleave_reads();
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   const bool vec_ok = true;  // host guarantees ldc % 8 == 0 and an aligned C

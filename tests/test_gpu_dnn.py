@@ -95,7 +95,7 @@ def test_norm_other_types(dnn, t, layer):
 @pytest.mark.parametrize("layer", [False, True])
 def test_norm_padded_rows(dnn, layer):
     y, ref, _ = run_norm(dnn, layer, BF16, 40, 1000, seed=9, pitch=1008)
-    assert np.max(np.abs(y - ref)) <= 1e-2
+    assert np.max(np.abs(y - ref)) <= 1e-2 * max(1.0, np.max(np.abs(ref)))
 
 
 def test_layernorm_constant_rows_give_beta_exactly(dnn):
