@@ -276,18 +276,18 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
   // the tile, and nothing waits for the data until the stage's barrier.
   const int lr = lane >> 3;
   const int pc = lane & 7;
-  auto issue_stage = [&](int kt, int st) {
+  // One DMA instruction: 1 KB (8 rows) of operand `op` for stage kt.
+  auto dma = [&](int kt, int st, int i, int op) {
     const int kb = kt * kFastKBytes;
-    const bool live = kt < ktiles;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int blk = 4 * i + wave;               // 8-row block index, 0..31
-      const int row = 8 * blk + lr;
-      const int c = pc ^ lr ^ (blk & 7);          // == pc ^ swz(row)
-      const bool ok = live && kb + 16 * c < kbytes;
+    const int blk = 4 * i + wave;               // 8-row block index, 0..31
+    const int row = 8 * blk + lr;
+    const int c = pc ^ lr ^ (blk & 7);          // == pc ^ swz(row)
+    const bool ok = kt < ktiles && kb + 16 * c < kbytes;
+    if (op == 0) {
       const uint32_t va = ok ? (uint32_t)(row * lda_b + 16 * c + kb) : kOff;
-      const uint32_t vb = ok ? (uint32_t)(row * ldb_b + 16 * c + kb) : kOff;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&lds[st][0][blk * 64], 16, va, 0, 0, 0);
+    } else {
+      const uint32_t vb = ok ? (uint32_t)(row * ldb_b + 16 * c + kb) : kOff;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&lds[st][1][blk * 64], 16, vb, 0, 0, 0);
     }
   };
@@ -310,71 +310,60 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
   // 16 bytes at logical chunk 2*ks + hh. Two register sets: the reads for
   // k-step ks+1 are in flight while the 16 MFMAs of k-step ks run.
   i32x4 fa[2][4], fb[2][4];
-  auto read_frags = [&](int st, int ks, int buf) {
+  auto frag = [&](int st, int ks, int buf, int q) {  // q: 0..3 A, 4..7 B
     const int kc = 2 * ks + hh;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    const int t = q & 3;
+    if (q < 4) {
       const int ar = wm * 128 + t * 32 + r32;
-      const int br = wn * 128 + t * 32 + r32;
       fa[buf][t] = lds[st][0][ar * kChunks + (kc ^ swz(ar))];
+    } else {
+      const int br = wn * 128 + t * 32 + r32;
       fb[buf][t] = lds[st][1][br * kChunks + (kc ^ swz(br))];
     }
   };
-  auto mma_step = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = Op::mma(fa[buf][i], fb[buf][j], acc[i][j]);
-  };
-  // Interleave: 8 LDS reads (next fragments), each behind one MFMA, then
-  // the remaining 8 MFMAs.
-  auto interleave_reads = [&]() {
+
+  // One k-step: 16 MFMAs on register set `buf`; behind every pair of MFMAs
+  // one fragment read for the next k-step and, in the phases that carry DMA,
+  // one DMA instruction. The explicit order, held by sched_barrier, keeps the
+  // wave from stalling on a burst of DMA issues while its matrix core idles.
+  auto phase = [&](int buf, int rd_st, int rd_ks, int dma_kt, int dma_st, int dma_half) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+      const int i = q >> 1, j0 = 2 * (q & 1);
+      acc[i][j0] = Op::mma(fa[buf][i], fb[buf][j0], acc[i][j0]);
+      acc[i][j0 + 1] = Op::mma(fa[buf][i], fb[buf][j0 + 1], acc[i][j0 + 1]);
+      frag(rd_st, rd_ks, buf ^ 1, q);
+      if (dma_half >= 0) dma(dma_kt, dma_st, 4 * dma_half + (q & 3), q >> 2);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   };
 
-  issue_stage(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // Stage s lives in LDS buffer s & 1. Iteration kt runs k-steps 0..2 of
+  // stage kt, one barrier, then k-step 3. Stage kt+2's DMA (into the buffer
+  // stage kt just vacated) is issued half right after that barrier and half
+  // during k-step 0 of the next iteration, so each load has two to four
+  // k-steps of MFMA time to land before the barrier that publishes it.
+#pragma unroll
+  for (int q = 0; q < 8; ++q) dma(0, 0, q & 3, q >> 2);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) dma(0, 0, 4 + (q & 3), q >> 2);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) dma(1, 1, q & 3, q >> 2);
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");   // stage 0 landed; stage 1 half 0 may fly
   __syncthreads();
-  read_frags(0, 0, 0);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) frag(0, 0, 0, q);
 
-  // Per stage: the DMA for stage kt+1 goes out first; k-steps 0..2 run with
-  // the next k-step's fragments loading behind them; then one barrier makes
-  // stage kt+1 visible (and retires every wave's reads of stage kt), and
-  // k-step 3 runs while the next stage's first fragments load.
   for (int kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
-    issue_stage(kt + 1, cur ^ 1);
-    read_frags(cur, 1, 1);
-    mma_step(0);
-    // k-step 0 also carries the 16 DMA issues of the next stage
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // 2 VMEM (DMA) issues
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(cur, 2, 0);
-    mma_step(1);
-    interleave_reads();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(cur, 3, 1);
-    mma_step(0);
-    interleave_reads();
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    phase(0, cur, 1, kt + 1, cur ^ 1, 1);
+    phase(1, cur, 2, 0, 0, -1);
+    phase(0, cur, 3, 0, 0, -1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 (both halves) landed
     __syncthreads();
-    read_frags(cur ^ 1, 0, 0);
-    mma_step(1);
-    interleave_reads();
-    __builtin_amdgcn_sched_barrier(0);
+    phase(1, cur ^ 1, 0, kt + 2, cur, 0);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // no LDS write may outlive the loop
 
   const bool vec_ok = true;  // host guarantees ldc % 8 == 0 and an aligned C
 #pragma unroll
