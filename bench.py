@@ -289,7 +289,21 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention")
+    ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy kernel of MIB MiB (torch), "
+                         "the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.calibration_copy:
+        import torch
+        n = args.calibration_copy * (1 << 20)
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_copy_bytes": n, "launches": 3}))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}).",
               file=sys.stderr)

@@ -36,6 +36,12 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
               "-I", os.path.join(ROCM, "include")]
 
+# Per-file extra flags. Attention keeps its MFMA results (scores and O) in
+# VGPRs, where the softmax VALU work reads them without AGPR copies.
+EXTRA = {
+    "kernels/attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 LIBS = {
     "libgrxrt.so": (["runtime.cpp"], []),
     "libgrxblas.so": (["grxblas.cpp", "kernels/gemm_mfma.hip", "kernels/sgemm.hip"], ["grxrt"]),
@@ -51,7 +57,7 @@ def _compile(src: str) -> str:
     path = os.path.join(CSRC, src)
     out = _obj(src)
     if src.endswith(".hip"):
-        cmd = [HIPCC, *HIP_FLAGS, *INCLUDES, "-c", path, "-o", out]
+        cmd = [HIPCC, *HIP_FLAGS, *EXTRA.get(src, []), *INCLUDES, "-c", path, "-o", out]
     else:
         cmd = ["g++", *HOST_FLAGS, *INCLUDES, "-c", path, "-o", out]
     r = subprocess.run(cmd, capture_output=True, text=True)

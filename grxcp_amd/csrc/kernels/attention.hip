@@ -4,24 +4,31 @@
 // (ref docs/designs/grxcp_roadmap.md:864-877). Single pass, online softmax,
 // O(S) memory:
 //
-//  * one workgroup = 4 wavefronts = 128 query rows of one (batch, head); each
-//    wave owns 32 queries whose Q fragment (32 x D bf16) stays in VGPRs;
-//  * K and V stream through LDS in 64-key tiles, double-buffered with the
-//    next tile's global loads in flight during the current tile's math;
-//  * scores are computed TRANSPOSED, S^T = K Q^T (v_mfma_f32_32x32x16): the
-//    accumulator then holds, per lane, 32 keys of ONE query, so the softmax
-//    row max/sum is an in-register reduction plus one exchange with the lane
-//    32 away, instead of a 32-lane shuffle tree;
-//  * O^T += V^T P^T (v_mfma again): P^T is already in the B-operand layout in
-//    the lanes that computed it (no LDS round trip for P); V is written to LDS
-//    transposed (key-contiguous, padded rows) so the A operand is two
-//    ds_read_b64 per step;
-//  * softmax in the exp2 domain: p = exp2(s*scale*log2e - m), with m tracked
-//    on raw scores; fp32 throughout; O is divided by the row sum once at the
-//    end and rounded to bf16/fp16 (RNE) once;
-//  * causal: key tiles past the query tile are never visited, only tiles that
-//    cross the diagonal are masked; workgroups are ordered heaviest first and
-//    all query tiles of a head run on one XCD (shared K/V in that XCD's L2).
+//  * one workgroup = 4 wavefronts = 256 query rows of one (batch, head); each
+//    wave owns 64 queries (two 32-query blocks) whose Q fragments stay in
+//    VGPRs, so every K or V fragment read from LDS feeds two MFMAs;
+//  * K and V stream through LDS in 64-key tiles by direct-to-LDS buffer loads
+//    (no staging registers; rows past the sequence read as zero), double
+//    buffered, the next tile's loads in flight during the current tile;
+//  * scores are computed TRANSPOSED, S^T = K Q^T (v_mfma_f32_32x32x16): per
+//    lane the accumulator holds 32 keys of ONE query, so the softmax row
+//    max/sum is an in-register reduction plus one exchange with lane^32;
+//  * O^T += V^T P^T: P^T is already in the B-operand layout in the lanes
+//    that computed it (no LDS round trip), and the V^T operand is read from
+//    the row-major V tile with ds_read_b64_tr_b16 (gfx950's transposing LDS
+//    read: 4 keys of one head-dim column per lane), so V is never rewritten;
+//  * softmax in the exp2 domain with the running max m tracked in scaled
+//    units: p = exp2(s*scale*log2e - m). m is only raised when a tile's max
+//    exceeds it by more than 8 (p <= 2^8 otherwise, exact in bf16's relative
+//    precision), so the O rescale (and its 128 multiplies) is rare;
+//  * P is packed with v_cvt_pk_bf16_f32 (round to nearest even); O is
+//    divided by the row sum once at the end and rounded once;
+//  * registers: this file is compiled with MFMA results in VGPRs
+//    (-amdgpu-mfma-vgpr-form) and Q parked in AGPRs, which keeps the scores,
+//    P and O out of AGPR<->VGPR copies;
+//  * causal: key tiles past the query tile are never loaded; a 32-query block
+//    skips tiles entirely above its diagonal; workgroups run heaviest first,
+//    and all query tiles of a head run on one XCD (K/V shared in its L2).
 
 #include "../launch.h"
 #include "device_common.h"
@@ -29,9 +36,12 @@
 namespace grxk {
 namespace {
 
-constexpr int kBQ = 128;          // queries per workgroup
-constexpr int kBK = 64;           // keys per tile
-constexpr int kVtPitch = kBK * 2 + 8;  // bytes per transposed-V row (padded)
+constexpr int kBQ = 256;  // queries per workgroup
+constexpr int kBK = 64;   // keys per tile
+constexpr uint32_t kRsrcWord3 = 0x00020000u;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_t;
 
 template <AttnType T> struct AIo;
 template <> struct AIo<AttnType::BF16> {
@@ -39,7 +49,12 @@ template <> struct AIo<AttnType::BF16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-  __device__ static uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
+  // two fp32 -> packed bf16 (RNE, v_cvt_pk_bf16_f32)
+  __device__ static uint32_t pack2(float a, float b) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
 };
 template <> struct AIo<AttnType::F16> {
   __device__ static f32x16 mma(i32x4 a, i32x4 b, f32x16 c) {
@@ -47,7 +62,9 @@ template <> struct AIo<AttnType::F16> {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
   __device__ static uint32_t pack2(float a, float b) {
-    return (uint32_t)f32_to_f16(a) | ((uint32_t)f32_to_f16(b) << 16);
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 
@@ -63,18 +80,32 @@ struct AParams {
   float c;  // scale * log2(e)
 };
 
+// K rows: ds_read_b128 of one logical chunk by 32 consecutive rows must hit
+// distinct banks; V rows: the 8 keys x 4 chunks of one transposing read must
+// spread evenly. Both are XOR swizzles of the 16-byte chunk index.
+template <int D> __device__ __forceinline__ int kswz(int row) {
+  if constexpr (D == 128) return row & 15;
+  else return (row ^ (row >> 3)) & 7;
+}
+template <int D> __device__ __forceinline__ int vswz(int row) {
+  if constexpr (D == 128) return 4 * (row & 3);
+  else return 4 * ((row >> 1) & 1);
+}
+
 template <AttnType T, int D>
-__global__ __launch_bounds__(256, 2) void attn_fwd(AParams p) {
+__global__ __launch_bounds__(256, 1) void attn_fwd(AParams p) {
   using IO = AIo<T>;
-  constexpr int DCH = D / 8;            // 16-byte chunks per K row
-  constexpr int DSTEPS = D / 16;        // MFMA k-steps over the head dim
-  constexpr int DT = D / 32;            // 32-wide output tiles over the head dim
-  __shared__ __attribute__((aligned(16))) i32x4 ks[2][kBK * DCH];
-  __shared__ __attribute__((aligned(16))) uint8_t vt[2][D * kVtPitch];
+  constexpr int CH = D / 8;          // 16-byte chunks per row
+  constexpr int RPI = 64 / CH;       // rows per 1 KB DMA instruction
+  constexpr int IPW = kBK / RPI / 4; // DMA instructions per wave per tensor per tile
+  constexpr int DSTEPS = D / 16;     // MFMA k-steps over the head dim
+  constexpr int DT = D / 32;         // 32-wide output tiles over the head dim
+  // [stage][K | V][key * CH + physical chunk]
+  __shared__ __attribute__((aligned(1024))) i32x4 lds[2][2][kBK * CH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
@@ -92,184 +123,211 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AParams p) {
   const uint8_t* kg = p.k + 2 * (b * p.k_sb + h * p.k_sh);
   const uint8_t* vg = p.v + 2 * (b * p.v_sb + h * p.v_sh);
   uint8_t* og = p.o + 2 * (b * p.o_sb + h * p.o_sh);
+  // Byte pitches and offsets are unsigned 32-bit: the host guarantees one
+  // head's rows span < 2^31 bytes; padding rows past S wrap harmlessly into
+  // range checks that read zero.
+  const uint32_t q_rs = (uint32_t)(2 * p.q_ss), k_rs = (uint32_t)(2 * p.k_ss), v_rs = (uint32_t)(2 * p.v_ss);
 
-  // Q fragment (B operand of S^T = K Q^T): query q0 + 32*wave + l32,
-  // head-dim elements 16*t + 8*hh .. +7.
-  const int myq = q0 + wave * 32 + l32;
-  i32x4 qf[DSTEPS];
+  // Row-ranged buffer descriptors: rows past S read as zero.
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)qg, (short)0, (int)((uint32_t)(p.S - 1) * q_rs + 2 * D), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)kg, (short)0, (int)((uint32_t)(p.S - 1) * k_rs + 2 * D), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)vg, (short)0, (int)((uint32_t)(p.S - 1) * v_rs + 2 * D), kRsrcWord3);
+
+  // Q fragments (B operand of S^T = K Q^T): block qb, query
+  // q0 + 64*wave + 32*qb + l32, head-dim elements 16*t + 8*hh .. +7.
+  int myq[2];
+  i32x4 qf[2][DSTEPS];
 #pragma unroll
-  for (int t = 0; t < DSTEPS; ++t) {
-    qf[t] = i32x4{0, 0, 0, 0};
-    if (myq < p.S) qf[t] = *(const i32x4*)(qg + 2 * ((int64_t)myq * p.q_ss + 16 * t + 8 * hh));
+  for (int qb = 0; qb < 2; ++qb) {
+    myq[qb] = q0 + 64 * wave + 32 * qb + l32;
+#pragma unroll
+    for (int t = 0; t < DSTEPS; ++t) {
+      qf[qb][t] = __builtin_amdgcn_raw_buffer_load_b128(
+          rq, (uint32_t)myq[qb] * q_rs + (uint32_t)(2 * (16 * t + 8 * hh)), 0, 0);
+      // Q is only ever an MFMA source operand, which may come from AGPRs:
+      // parking it there leaves the VGPRs to the scores, P and O.
+      asm volatile("" : "+a"(qf[qb][t]));
+    }
   }
 
   const int kv_end = p.causal ? min(p.S, q0 + kBQ) : p.S;
   const int ntiles = (kv_end + kBK - 1) / kBK;
 
-  // K loader: 64 rows x DCH chunks, swizzled chunk = c ^ (row & 15).
-  constexpr int KCH_PER_T = kBK * DCH / 256;
-  // V loader: key pair kp (0..31) x head-dim chunk dc: reads keys 2kp, 2kp+1
-  // and writes 8 packed (key, key+1) words into the transposed tile.
-  constexpr int VT_PER_T = (kBK / 2) * DCH / 256;
-  i32x4 kr[KCH_PER_T];
-  i32x4 vr[VT_PER_T][2];
-
-  auto load_tile = [&](int t) {
+  // DMA: instruction i of wave w fills rows RPI*(IPW*w + i) .. of K or V;
+  // lane L lands in row +L/CH at physical chunk L%CH.
+  auto dma_tile = [&](int t, int st) {
     const int kv0 = t * kBK;
 #pragma unroll
-    for (int i = 0; i < KCH_PER_T; ++i) {
-      const int e = tid + 256 * i;
-      const int row = e / DCH, c = e % DCH;
-      const int key = kv0 + row;
-      kr[i] = i32x4{0, 0, 0, 0};
-      if (key < p.S) kr[i] = *(const i32x4*)(kg + 2 * ((int64_t)key * p.k_ss + 8 * c));
-    }
-#pragma unroll
-    for (int i = 0; i < VT_PER_T; ++i) {
-      const int e = tid + 256 * i;
-      const int kp = e % (kBK / 2), dc = e / (kBK / 2);
-      const int key = kv0 + 2 * kp;
-      vr[i][0] = i32x4{0, 0, 0, 0};
-      vr[i][1] = i32x4{0, 0, 0, 0};
-      if (key < p.S) vr[i][0] = *(const i32x4*)(vg + 2 * ((int64_t)key * p.v_ss + 8 * dc));
-      if (key + 1 < p.S) vr[i][1] = *(const i32x4*)(vg + 2 * ((int64_t)(key + 1) * p.v_ss + 8 * dc));
-    }
-  };
-  auto store_tile = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < KCH_PER_T; ++i) {
-      const int e = tid + 256 * i;
-      const int row = e / DCH, c = e % DCH;
-      ks[st][row * DCH + (c ^ ((row & 15) % DCH))] = kr[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VT_PER_T; ++i) {
-      const int e = tid + 256 * i;
-      const int kp = e % (kBK / 2), dc = e / (kBK / 2);
-      const u32x4 a = __builtin_bit_cast(u32x4, vr[i][0]);
-      const u32x4 c = __builtin_bit_cast(u32x4, vr[i][1]);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = (a[w] & 0xffffu) | (c[w] << 16);
-        const uint32_t hi = (a[w] >> 16) | (c[w] & 0xffff0000u);
-        *(uint32_t*)(vt[st] + (8 * dc + 2 * w) * kVtPitch + 4 * kp) = lo;
-        *(uint32_t*)(vt[st] + (8 * dc + 2 * w + 1) * kVtPitch + 4 * kp) = hi;
-      }
+    for (int i = 0; i < IPW; ++i) {
+      const int blk = IPW * wave + i;
+      const int row = RPI * blk + lane / CH;
+      const int pc = lane % CH;
+      const bool ok = t < ntiles;
+      const uint32_t kr = (uint32_t)(kv0 + row);
+      const uint32_t ko = ok ? kr * k_rs + (uint32_t)(16 * (pc ^ kswz<D>(row))) : 0x80000000u;
+      const uint32_t vo = ok ? kr * v_rs + (uint32_t)(16 * (pc ^ vswz<D>(row))) : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)&lds[st][0][blk * 64], 16, ko, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)&lds[st][1][blk * 64], 16, vo, 0, 0, 0);
     }
   };
 
-  f32x16 o_acc[DT];
+  f32x16 o_acc[2][DT];
 #pragma unroll
-  for (int i = 0; i < DT; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.0f;
-  float m_run = -INFINITY;  // running max of raw scores for query myq
-  float l_run = 0.0f;       // this half-wave's share of the running sum
-
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int cur = t & 1;
-    const bool more = t + 1 < ntiles;
-    if (more) load_tile(t + 1);
-    const int kv0 = t * kBK;
-
-    // S^T tile: two 32-key blocks x 32 queries.
-    f32x16 s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
-      const int row = kb * 32 + l32;
-#pragma unroll
-      for (int d = 0; d < DSTEPS; ++d) {
-        const int c = 2 * d + hh;
-        const i32x4 kf = ks[cur][row * DCH + (c ^ ((row & 15) % DCH))];
-        s[kb] = IO::mma(kf, qf[d], s[kb]);
-      }
-    }
-
-    // Mask keys past the sequence end and (causal) past the query.
-    const bool need_mask = (kv0 + kBK > p.S) || (p.causal && kv0 + kBK - 1 > q0 + wave * 32);
-    if (need_mask) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kv0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key >= p.S || (p.causal && key > myq)) s[kb][r] = -INFINITY;
-        }
-    }
-
-    // Online softmax for this lane's query (other half of its keys in lane^32).
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * p.c);
-    m_run = m_new;
-    const float mc = m_use * p.c;
-    float psum = 0.0f;
-    uint32_t pk[2][8];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kb][r], p.c, -mc));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kb][r + 1], p.c, -mc));
-        psum += p0 + p1;
-        pk[kb][r >> 1] = IO::pack2(p0, p1);
-      }
-    l_run = l_run * alpha + psum;
+  for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
     for (int i = 0; i < DT; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+      for (int r = 0; r < 16; ++r) o_acc[qb][i][r] = 0.0f;
+  float m_run[2] = {-INFINITY, -INFINITY};  // running max, scaled (log2) units
+  float l_run[2] = {0.0f, 0.0f};            // this half-wave's share of the sum
 
-    // O^T += V^T P^T over the 64 keys, 16 keys per MFMA step.
+  dma_tile(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // Transposed-read addressing for V^T (A operand of O^T = V^T P^T): lane l
+  // supplies head-dim row d = 32*dt + l32 and keys {16st + 4hh + r} (first
+  // read) and {16st + 8 + 4hh + r} (second read), r = 0..3. Source lane
+  // s = l%16 of its 16-lane group points at key 16st + 4hh + s/4 (+8),
+  // head-dim 32*dt + 16*((l>>4)&1) + 4*(s&3).
+  const int tr_key = 4 * hh + ((lane & 15) >> 2);
+  const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int cur = t & 1;
+    dma_tile(t + 1, cur ^ 1);
+    const int kv0 = t * kBK;
+    const i32x4* kt = &lds[cur][0][0];
+    const uint8_t* vt = (const uint8_t*)&lds[cur][1][0];
+
+    // A wave whose 64 queries all precede this tile skips it (causal); the
+    // DMA it issued above and the barrier below are still its share.
+    const bool wave_live = !p.causal || kv0 <= q0 + 64 * wave + 63;
+    if (wave_live) {
+      // S^T tiles: [qb][key block], 32 keys x 32 queries each; every K
+      // fragment feeds both query blocks.
+      f32x16 s[2][2];
 #pragma unroll
-    for (int st = 0; st < kBK / 16; ++st) {
-      const int kb = st >> 1;
-      const int half = st & 1;
-      const i32x4 pf = i32x4{(int)pk[kb][4 * half + 0], (int)pk[kb][4 * half + 1],
-                             (int)pk[kb][4 * half + 2], (int)pk[kb][4 * half + 3]};
+      for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const uint8_t* vrow = vt[cur] + (dt * 32 + l32) * kVtPitch;
-        const u32x2 v0 = *(const u32x2*)(vrow + 2 * (16 * st + 4 * hh));
-        const u32x2 v1 = *(const u32x2*)(vrow + 2 * (16 * st + 8 + 4 * hh));
-        const i32x4 vf = i32x4{(int)v0.x, (int)v0.y, (int)v1.x, (int)v1.y};
-        o_acc[dt] = IO::mma(vf, pf, o_acc[dt]);
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[qb][kb][r] = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int row = kb * 32 + l32;
+#pragma unroll
+        for (int d = 0; d < DSTEPS; ++d) {
+          const int c = 2 * d + hh;
+          const i32x4 kf = kt[row * CH + (c ^ kswz<D>(row))];
+          s[0][kb] = IO::mma(kf, qf[0][d], s[0][kb]);
+          s[1][kb] = IO::mma(kf, qf[1][d], s[1][kb]);
+        }
+      }
+
+      // Keys past the sequence end, and (causal) past the query, are masked
+      // only on tiles that can contain such keys for this wave.
+      const bool need_mask = (kv0 + kBK > p.S) || (p.causal && kv0 + kBK - 1 > q0 + 64 * wave);
+      if (need_mask) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = kv0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+              const bool masked = key >= p.S || (p.causal && key > myq[qb]);
+              s[qb][kb][r] = masked ? -INFINITY : s[qb][kb][r];
+            }
+      }
+
+      // Online softmax for this lane's two queries.
+      uint32_t pk[2][2][8];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * p.c;
+        // Raise the running max only when this tile exceeds it by > 8.
+        const bool raise = mx > m_run[qb] + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(raise)) {
+          const float m_new = raise ? mx : m_run[qb];
+          const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+          m_run[qb] = m_new;
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int i = 0; i < DT; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o_acc[qb][i][r] *= alpha;
+        }
+        const float m = m_run[qb];
+        float psum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][r], p.c, -m));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][r + 1], p.c, -m));
+            psum += p0 + p1;
+            pk[qb][kb][r >> 1] = IO::pack2(p0, p1);
+          }
+        l_run[qb] += psum;
+      }
+
+      // O^T += V^T P^T, 16 keys per MFMA step; one V^T fragment feeds both
+      // query blocks.
+#pragma unroll
+      for (int st = 0; st < kBK / 16; ++st) {
+        const int kb = st >> 1, half = st & 1;
+        i32x4 pf[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          pf[qb] = i32x4{(int)pk[qb][kb][4 * half + 0], (int)pk[qb][kb][4 * half + 1],
+                         (int)pk[qb][kb][4 * half + 2], (int)pk[qb][kb][4 * half + 3]};
+        const int k1 = 16 * st + tr_key, k2 = k1 + 8;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int d = 32 * dt + tr_d;  // element column; 8-byte aligned
+          const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_t)(vt + k1 * (2 * D) + 16 * ((d >> 3) ^ vswz<D>(k1)) + 2 * (d & 7)));
+          const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_t)(vt + k2 * (2 * D) + 16 * ((d >> 3) ^ vswz<D>(k2)) + 2 * (d & 7)));
+          const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+          const i32x4 vf = i32x4{(int)w0.x, (int)w0.y, (int)w1.x, (int)w1.y};
+          o_acc[0][dt] = IO::mma(vf, pf[0], o_acc[0][dt]);
+          o_acc[1][dt] = IO::mma(vf, pf[1], o_acc[1][dt]);
+        }
       }
     }
 
-    if (more) store_tile(cur ^ 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next tile's DMA landed
     __syncthreads();
   }
 
-  // O[myq, d] = O^T[d, myq] / l; lane holds d = 32*dt + 8*g + 4*hh + 0..3.
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (myq < p.S) {
-    uint8_t* orow = og + 2 * (int64_t)myq * p.o_ss;
+  // O[q, d] = O^T[d, q] / l; lane holds d = 32*dt + 8*g + 4*hh + 0..3.
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int qb = 0; qb < 2; ++qb) {
+    const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
+    const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (myq[qb] < p.S) {
+      uint8_t* orow = og + 2 * (int64_t)myq[qb] * p.o_ss;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = dt * 32 + 8 * g + 4 * hh;
-        u32x2 w;
-        w.x = IO::pack2(o_acc[dt][4 * g + 0] * inv_l, o_acc[dt][4 * g + 1] * inv_l);
-        w.y = IO::pack2(o_acc[dt][4 * g + 2] * inv_l, o_acc[dt][4 * g + 3] * inv_l);
-        *(u32x2*)(orow + 2 * d) = w;
-      }
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = dt * 32 + 8 * g + 4 * hh;
+          u32x2 w;
+          w.x = IO::pack2(o_acc[qb][dt][4 * g + 0] * inv_l, o_acc[qb][dt][4 * g + 1] * inv_l);
+          w.y = IO::pack2(o_acc[qb][dt][4 * g + 2] * inv_l, o_acc[qb][dt][4 * g + 3] * inv_l);
+          *(u32x2*)(orow + 2 * d) = w;
+        }
+    }
   }
 }
 
@@ -286,6 +344,11 @@ hipError_t run(const AttnDesc& d, hipStream_t s) {
   p.qtiles = (d.S + kBQ - 1) / kBQ;
   p.causal = d.causal ? 1 : 0;
   p.c = d.scale * 1.4426950408889634f;
+  // 32-bit buffer offsets within one head: (S-1) * row pitch + row < 2^31.
+  int64_t pitch = d.q_ss > d.k_ss ? d.q_ss : d.k_ss;
+  pitch = pitch > d.v_ss ? pitch : d.v_ss;
+  const int64_t span = ((int64_t)d.S + kBQ) * 2 * pitch + 2 * d.D;
+  if (span >= (1ll << 31)) return hipErrorNotSupported;
   const int64_t blocks = (int64_t)d.B * d.H * p.qtiles;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL((attn_fwd<T, D>), dim3((unsigned)blocks), dim3(256), 0, s, p);
