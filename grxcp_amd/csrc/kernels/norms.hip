@@ -5,11 +5,13 @@
 // read once and every byte of y written once, so the design goal is streaming
 // bandwidth, not arithmetic.
 //
-//  * one row per 256-thread workgroup (4 wavefronts); thousands of rows give
-//    far more than the 256 CUs x 8 resident workgroups needed to keep HBM busy;
-//  * the row is held in registers between the statistics pass and the output
-//    pass (up to 8 x 16-byte chunks per thread = 16384 bf16 elements), so x is
-//    read from HBM exactly once; longer rows re-read x (from L2);
+//  * rows of up to 1024 16-byte chunks (8192 bf16): one row per 64-lane
+//    wavefront, held packed in registers between the statistics pass and the
+//    output pass; both statistics are shuffle reductions, so there is no LDS
+//    and no barrier and every wave streams independently;
+//  * longer rows (up to 2048 chunks): one row per 256-thread workgroup, with
+//    a 4-entry LDS combine; x is still read from HBM exactly once;
+//  * longer still: x re-read per pass (from L2);
 //  * 16-byte non-temporal loads of x and stores of y, gamma/beta via the
 //    normal cached path (every row reuses them);
 //  * statistics in fp32: wavefront butterfly (__shfl_xor) then a 4-entry LDS
@@ -49,9 +51,15 @@ template <> struct Io<NormType::BF16> {
     }
   }
   __device__ static u32x4 pack(const float* f) {
+    // v_cvt_pk_bf16_f32: round to nearest even, NaN quieted -- the same
+    // bits as f32_to_bf16.
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     u32x4 w;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) w[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
+    for (int q = 0; q < 4; ++q) {
+      const bf16x2 v = {(__bf16)f[2 * q], (__bf16)f[2 * q + 1]};
+      w[q] = __builtin_bit_cast(uint32_t, v);
+    }
     return w;
   }
 };
@@ -169,6 +177,84 @@ __global__ __launch_bounds__(256) void norm_vec(NParams p) {
   }
 }
 
+// One row per 64-lane wavefront, for rows of up to NC x 64 16-byte chunks:
+// the row lives in the wave's registers, both statistics are wave
+// reductions (shuffles only: no LDS, no barrier), so every wave streams
+// independently and a CU keeps ~20 rows of loads in flight.
+template <NormType T, bool LAYER, int NC>
+__global__ __launch_bounds__(256) void norm_wave(NParams p) {
+  using IO = Io<T>;
+  constexpr int V = IO::kVec;
+  const int lane = threadIdx.x & 63;
+  const int nchunks = p.hidden / V;
+  const float inv_h = 1.0f / (float)p.hidden;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < p.rows; row += nwaves) {
+    const uint8_t* xrow = p.x + row * p.x_rs * (int64_t)(16 / V);
+    uint8_t* yrow = p.y + row * p.y_rs * (int64_t)(16 / V);
+    u32x4 raw[NC];
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+      const int c = lane + 64 * q;
+      raw[q] = c < nchunks ? __builtin_nontemporal_load((const u32x4*)xrow + c) : u32x4{0, 0, 0, 0};
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+      float v[V];
+      IO::unpack(raw[q], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e) s += LAYER ? v[e] : v[e] * v[e];
+    }
+    // Keep only the packed row live between passes (unpacking again is a
+    // couple of ALU ops; holding 8*NC floats would halve the waves per CU).
+#pragma unroll
+    for (int q = 0; q < NC; ++q) asm volatile("" : "+v"(raw[q]));
+    s = wave_sum(s);
+    float mean = 0.0f, inv;
+    if (LAYER) {
+      mean = s * inv_h;
+      float d2 = 0.0f;
+#pragma unroll
+      for (int q = 0; q < NC; ++q) {
+        if (lane + 64 * q >= nchunks) continue;
+        float v[V];
+        IO::unpack(raw[q], v);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float d = v[e] - mean;
+          d2 += d * d;
+        }
+      }
+      d2 = wave_sum(d2);
+#pragma unroll
+      for (int q = 0; q < NC; ++q) asm volatile("" : "+v"(raw[q]));
+      inv = 1.0f / sqrtf(d2 * inv_h + p.eps);
+    } else {
+      inv = 1.0f / sqrtf(s * inv_h + p.eps);
+    }
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+      const int c = lane + 64 * q;
+      if (c >= nchunks) continue;
+      float v[V], g[V], o[V];
+      IO::unpack(raw[q], v);
+      IO::unpack(((const u32x4*)p.gamma)[c], g);
+      if (LAYER) {
+        float b[V];
+        IO::unpack(((const u32x4*)p.beta)[c], b);
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[e] = (v[e] - mean) * inv * g[e] + b[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[e] = v[e] * inv * g[e];
+      }
+      __builtin_nontemporal_store(IO::pack(o), (u32x4*)yrow + c);
+    }
+  }
+}
+
 // Any length / alignment: element-wise, x re-read for each pass.
 template <NormType T, bool LAYER>
 __global__ __launch_bounds__(256) void norm_scalar(NParams p) {
@@ -224,7 +310,18 @@ hipError_t run(const NormDesc& d, hipStream_t s) {
   const bool vec = d.hidden % V == 0 && d.x_row_stride % V == 0 && d.y_row_stride % V == 0 &&
                    al(d.x) && al(d.y) && al(d.gamma) && (!LAYER || al(d.beta));
   const int nchunks = d.hidden / V;
-  if (vec && nchunks <= 256) {
+  const unsigned wgrid = (unsigned)std::min<int64_t>((d.rows + 3) / 4, 1 << 30);
+  if (vec && nchunks <= 64) {
+    hipLaunchKernelGGL((norm_wave<T, LAYER, 1>), dim3(wgrid), dim3(256), 0, s, p);
+  } else if (vec && nchunks <= 128) {
+    hipLaunchKernelGGL((norm_wave<T, LAYER, 2>), dim3(wgrid), dim3(256), 0, s, p);
+  } else if (vec && nchunks <= 256) {
+    hipLaunchKernelGGL((norm_wave<T, LAYER, 4>), dim3(wgrid), dim3(256), 0, s, p);
+  } else if (vec && nchunks <= 512) {
+    hipLaunchKernelGGL((norm_wave<T, LAYER, 8>), dim3(wgrid), dim3(256), 0, s, p);
+  } else if (vec && nchunks <= 1024) {
+    hipLaunchKernelGGL((norm_wave<T, LAYER, 16>), dim3(wgrid), dim3(256), 0, s, p);
+  } else if (vec && nchunks <= 256) {
     hipLaunchKernelGGL((norm_vec<T, LAYER, 1>), dim3(grid), dim3(256), 0, s, p);
   } else if (vec && nchunks <= 512) {
     hipLaunchKernelGGL((norm_vec<T, LAYER, 2>), dim3(grid), dim3(256), 0, s, p);
