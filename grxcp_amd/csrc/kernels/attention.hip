@@ -36,12 +36,41 @@
 namespace grxk {
 namespace {
 
-constexpr int kBQ = 256;  // queries per workgroup
+constexpr int kNW = 8;          // wavefronts per workgroup (two per SIMD)
+constexpr int kBQ = 32 * kNW;   // queries per workgroup, 32 per wave
 constexpr int kBK = 64;   // keys per tile
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_t;
+template <int N> struct Stage { static constexpr int value = N; };
+
+// Buffer descriptor words: 48-bit base, stride 0, num_records bytes (reads
+// past it return zero), raw-buffer format word.
+__device__ __forceinline__ i32x4 rsrc_words(const void* base, uint32_t num_records) {
+  const uint64_t a = (uint64_t)base;
+  return i32x4{(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xffff, (int)num_records, (int)kRsrcWord3};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr_t)p;
+}
+// 16 bytes per lane from global memory straight into LDS (lane L writes
+// lds + 16*L). Issued as assembly so that the compiler does not see an LDS
+// write: it would otherwise make every later transposing LDS read wait for
+// ALL outstanding DMA, including the prefetch of the next tile. Ordering is
+// explicit instead: each tile ends with s_waitcnt vmcnt(0) and a barrier
+// before any wave reads the stage this DMA fills. M0 carries the LDS base;
+// no other instruction in the attention kernel uses M0.
+// s_waitcnt vmcnt(0) through the builtin, so that the compiler's own wait
+// bookkeeping also sees every earlier load as complete.
+__device__ __forceinline__ void wait_vmem_all() {
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt 0, expcnt 7, lgkmcnt 15: wait on vmcnt only
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds), "v"(voff), "s"(rsrc) : "memory");
+}
 
 template <AttnType T> struct AIo;
 template <> struct AIo<AttnType::BF16> {
@@ -55,6 +84,12 @@ template <> struct AIo<AttnType::BF16> {
     const bf16x2 v = {(__bf16)a, (__bf16)b};
     return __builtin_bit_cast(uint32_t, v);
   }
+  // acc + the two packed values (v_dot2_f32_bf16 against (1, 1))
+  __device__ static float sum2(uint32_t packed, float acc) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), one, acc, false);
+  }
 };
 template <> struct AIo<AttnType::F16> {
   __device__ static f32x16 mma(i32x4 a, i32x4 b, f32x16 c) {
@@ -65,6 +100,11 @@ template <> struct AIo<AttnType::F16> {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     const f16x2 v = {(_Float16)a, (_Float16)b};
     return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static float sum2(uint32_t packed, float acc) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), one, acc, false);
   }
 };
 
@@ -92,14 +132,28 @@ template <int D> __device__ __forceinline__ int vswz(int row) {
   else return 4 * ((row >> 1) & 1);
 }
 
+// Value from the other half of the wave (lane ^ 32): v_permlane32_swap
+// exchanges the upper half of its first operand with the lower half of its
+// second; with both operands = x, lane l of the two results holds x[l] and
+// x[l ^ 32] in some order.
+__device__ __forceinline__ float half_swap_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <AttnType T, int D>
-__global__ __launch_bounds__(256, 1) void attn_fwd(AParams p) {
+__global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
   using IO = AIo<T>;
-  constexpr int CH = D / 8;          // 16-byte chunks per row
-  constexpr int RPI = 64 / CH;       // rows per 1 KB DMA instruction
-  constexpr int IPW = kBK / RPI / 4; // DMA instructions per wave per tensor per tile
-  constexpr int DSTEPS = D / 16;     // MFMA k-steps over the head dim
-  constexpr int DT = D / 32;         // 32-wide output tiles over the head dim
+  constexpr int CH = D / 8;            // 16-byte chunks per row
+  constexpr int RPI = 64 / CH;         // rows per 1 KB DMA instruction
+  constexpr int IPW = kBK / RPI / kNW; // DMA instructions per wave per tensor per tile
+  constexpr int DSTEPS = D / 16;       // MFMA k-steps over the head dim
+  constexpr int DT = D / 32;           // 32-wide output tiles over the head dim
+  static_assert(IPW >= 1, "tile too small for the wave count");
   // [stage][K | V][key * CH + physical chunk]
   __shared__ __attribute__((aligned(1024))) i32x4 lds[2][2][kBK * CH];
 
@@ -118,6 +172,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd(AParams p) {
   const int qt = p.causal ? (p.qtiles - 1 - logical % p.qtiles) : (logical % p.qtiles);
   const int b = bh / p.H, h = bh % p.H;
   const int q0 = qt * kBQ;
+  const int wq0 = q0 + 32 * wave;  // this wave's first query
 
   const uint8_t* qg = p.q + 2 * (b * p.q_sb + h * p.q_sh);
   const uint8_t* kg = p.k + 2 * (b * p.k_sb + h * p.k_sh);
@@ -131,26 +186,17 @@ __global__ __launch_bounds__(256, 1) void attn_fwd(AParams p) {
   // Row-ranged buffer descriptors: rows past S read as zero.
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
       (void*)qg, (short)0, (int)((uint32_t)(p.S - 1) * q_rs + 2 * D), kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)kg, (short)0, (int)((uint32_t)(p.S - 1) * k_rs + 2 * D), kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)vg, (short)0, (int)((uint32_t)(p.S - 1) * v_rs + 2 * D), kRsrcWord3);
+  const i32x4 rk = rsrc_words(kg, (uint32_t)(p.S - 1) * k_rs + 2 * D);
+  const i32x4 rv = rsrc_words(vg, (uint32_t)(p.S - 1) * v_rs + 2 * D);
 
-  // Q fragments (B operand of S^T = K Q^T): block qb, query
-  // q0 + 64*wave + 32*qb + l32, head-dim elements 16*t + 8*hh .. +7.
-  int myq[2];
-  i32x4 qf[2][DSTEPS];
+  // Q fragments (B operand of S^T = K Q^T): query wq0 + l32, head-dim
+  // elements 16*t + 8*hh .. +7.
+  const int myq = wq0 + l32;
+  i32x4 qf[DSTEPS];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    myq[qb] = q0 + 64 * wave + 32 * qb + l32;
-#pragma unroll
-    for (int t = 0; t < DSTEPS; ++t) {
-      qf[qb][t] = __builtin_amdgcn_raw_buffer_load_b128(
-          rq, (uint32_t)myq[qb] * q_rs + (uint32_t)(2 * (16 * t + 8 * hh)), 0, 0);
-      // Q is only ever an MFMA source operand, which may come from AGPRs:
-      // parking it there leaves the VGPRs to the scores, P and O.
-      asm volatile("" : "+a"(qf[qb][t]));
-    }
+  for (int t = 0; t < DSTEPS; ++t) {
+    qf[t] = __builtin_amdgcn_raw_buffer_load_b128(
+        rq, (uint32_t)myq * q_rs + (uint32_t)(2 * (16 * t + 8 * hh)), 0, 0);
   }
 
   const int kv_end = p.causal ? min(p.S, q0 + kBQ) : p.S;
@@ -169,23 +215,21 @@ __global__ __launch_bounds__(256, 1) void attn_fwd(AParams p) {
       const uint32_t kr = (uint32_t)(kv0 + row);
       const uint32_t ko = ok ? kr * k_rs + (uint32_t)(16 * (pc ^ kswz<D>(row))) : 0x80000000u;
       const uint32_t vo = ok ? kr * v_rs + (uint32_t)(16 * (pc ^ vswz<D>(row))) : 0x80000000u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)&lds[st][0][blk * 64], 16, ko, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)&lds[st][1][blk * 64], 16, vo, 0, 0, 0);
+      dma16(rk, lds_addr(&lds[st][0][blk * 64]), ko);
+      dma16(rv, lds_addr(&lds[st][1][blk * 64]), vo);
     }
   };
 
-  f32x16 o_acc[2][DT];
+  f32x16 o_acc[DT];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int i = 0; i < DT; ++i)
 #pragma unroll
-    for (int i = 0; i < DT; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o_acc[qb][i][r] = 0.0f;
-  float m_run[2] = {-INFINITY, -INFINITY};  // running max, scaled (log2) units
-  float l_run[2] = {0.0f, 0.0f};            // this half-wave's share of the sum
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.0f;
+  float m_run = -INFINITY;  // running max, scaled (log2) units
+  float l_run = 0.0f;       // this half-wave's share of the sum
 
   dma_tile(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  wait_vmem_all();  // Q fragments and the first tile
   __syncthreads();
 
   // Transposed-read addressing for V^T (A operand of O^T = V^T P^T): lane l
@@ -196,100 +240,93 @@ __global__ __launch_bounds__(256, 1) void attn_fwd(AParams p) {
   const int tr_key = 4 * hh + ((lane & 15) >> 2);
   const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int cur = t & 1;
+  // One 64-key tile; the LDS stage is a compile-time constant so every LDS
+  // address is a loop-invariant register plus an immediate offset.
+  auto tile = [&](auto stage, int t) {
+    constexpr int cur = decltype(stage)::value;
     dma_tile(t + 1, cur ^ 1);
     const int kv0 = t * kBK;
     const i32x4* kt = &lds[cur][0][0];
     const uint8_t* vt = (const uint8_t*)&lds[cur][1][0];
 
-    // A wave whose 64 queries all precede this tile skips it (causal); the
+    // A wave whose 32 queries all precede this tile skips it (causal); the
     // DMA it issued above and the barrier below are still its share.
-    const bool wave_live = !p.causal || kv0 <= q0 + 64 * wave + 63;
+    const bool wave_live = !p.causal || kv0 <= wq0 + 31;
     if (wave_live) {
-      // S^T tiles: [qb][key block], 32 keys x 32 queries each; every K
-      // fragment feeds both query blocks.
-      f32x16 s[2][2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[qb][kb][r] = 0.0f;
+      // S^T tiles: [key block], 32 keys x 32 queries each. The K fragments
+      // of a key block are all read before its MFMAs.
+      f32x16 s[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int row = kb * 32 + l32;
+        i32x4 kf[DSTEPS];
 #pragma unroll
-        for (int d = 0; d < DSTEPS; ++d) {
-          const int c = 2 * d + hh;
-          const i32x4 kf = kt[row * CH + (c ^ kswz<D>(row))];
-          s[0][kb] = IO::mma(kf, qf[0][d], s[0][kb]);
-          s[1][kb] = IO::mma(kf, qf[1][d], s[1][kb]);
-        }
+        for (int d = 0; d < DSTEPS; ++d) kf[d] = kt[row * CH + ((2 * d + hh) ^ kswz<D>(row))];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < DSTEPS; ++d) s[kb] = IO::mma(kf[d], qf[d], s[kb]);
       }
 
       // Keys past the sequence end, and (causal) past the query, are masked
       // only on tiles that can contain such keys for this wave.
-      const bool need_mask = (kv0 + kBK > p.S) || (p.causal && kv0 + kBK - 1 > q0 + 64 * wave);
+      const bool need_mask = (kv0 + kBK > p.S) || (p.causal && kv0 + kBK - 1 > wq0);
       if (need_mask) {
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = kv0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-              const bool masked = key >= p.S || (p.causal && key > myq[qb]);
-              s[qb][kb][r] = masked ? -INFINITY : s[qb][kb][r];
-            }
-      }
-
-      // Online softmax for this lane's two queries.
-      uint32_t pk[2][2][8];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        float mx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * p.c;
+          for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+            const bool masked = key >= p.S || (p.causal && key > myq);
+            s[kb][r] = masked ? -INFINITY : s[kb][r];
+          }
+      }
+
+      // Online softmax for this lane's query.
+      uint32_t pk[2][8];
+      {
+        float mx0 = -INFINITY, mx1 = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          mx0 = fmaxf(mx0, s[0][r]);
+          mx1 = fmaxf(mx1, s[1][r]);
+        }
+        const float mx = half_swap_max(fmaxf(mx0, mx1)) * p.c;
         // Raise the running max only when this tile exceeds it by > 8.
-        const bool raise = mx > m_run[qb] + 8.0f;
+        const bool raise = mx > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(raise)) {
-          const float m_new = raise ? mx : m_run[qb];
-          const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-          m_run[qb] = m_new;
-          l_run[qb] *= alpha;
+          const float m_new = raise ? mx : m_run;
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+          m_run = m_new;
+          l_run *= alpha;
 #pragma unroll
           for (int i = 0; i < DT; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o_acc[qb][i][r] *= alpha;
+            for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
         }
-        const float m = m_run[qb];
-        float psum = 0.0f;
+        const float m = m_run;
+        // The row sum adds the ROUNDED probabilities (v_dot2 over the packed
+        // pairs), the same values the O update multiplies.
+        float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; r += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][r], p.c, -m));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][r + 1], p.c, -m));
-            psum += p0 + p1;
-            pk[qb][kb][r >> 1] = IO::pack2(p0, p1);
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kb][r], p.c, -m));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kb][r + 1], p.c, -m));
+            pk[kb][r >> 1] = IO::pack2(p0, p1);
+            if (kb == 0) ps0 = IO::sum2(pk[kb][r >> 1], ps0);
+            else ps1 = IO::sum2(pk[kb][r >> 1], ps1);
           }
-        l_run[qb] += psum;
+        l_run += ps0 + ps1;
       }
 
-      // O^T += V^T P^T, 16 keys per MFMA step; one V^T fragment feeds both
-      // query blocks.
+      // O^T += V^T P^T, 16 keys per MFMA step.
 #pragma unroll
       for (int st = 0; st < kBK / 16; ++st) {
         const int kb = st >> 1, half = st & 1;
-        i32x4 pf[2];
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-          pf[qb] = i32x4{(int)pk[qb][kb][4 * half + 0], (int)pk[qb][kb][4 * half + 1],
-                         (int)pk[qb][kb][4 * half + 2], (int)pk[qb][kb][4 * half + 3]};
+        const i32x4 pf = i32x4{(int)pk[kb][4 * half + 0], (int)pk[kb][4 * half + 1],
+                               (int)pk[kb][4 * half + 2], (int)pk[kb][4 * half + 3]};
         const int k1 = 16 * st + tr_key, k2 = k1 + 8;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
@@ -300,34 +337,34 @@ __global__ __launch_bounds__(256, 1) void attn_fwd(AParams p) {
               (lds_s16x4_t)(vt + k2 * (2 * D) + 16 * ((d >> 3) ^ vswz<D>(k2)) + 2 * (d & 7)));
           const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
           const i32x4 vf = i32x4{(int)w0.x, (int)w0.y, (int)w1.x, (int)w1.y};
-          o_acc[0][dt] = IO::mma(vf, pf[0], o_acc[0][dt]);
-          o_acc[1][dt] = IO::mma(vf, pf[1], o_acc[1][dt]);
+          o_acc[dt] = IO::mma(vf, pf, o_acc[dt]);
         }
       }
     }
 
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next tile's DMA landed
+    wait_vmem_all();  // next tile's DMA landed
     __syncthreads();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    tile(Stage<0>{}, t);
+    if (t + 1 < ntiles) tile(Stage<1>{}, t + 1);
   }
 
   // O[q, d] = O^T[d, q] / l; lane holds d = 32*dt + 8*g + 4*hh + 0..3.
+  const float l_tot = half_swap_sum(l_run);
+  const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (myq < p.S) {
+    uint8_t* orow = og + 2 * (int64_t)myq * p.o_ss;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
-    const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (myq[qb] < p.S) {
-      uint8_t* orow = og + 2 * (int64_t)myq[qb] * p.o_ss;
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d = dt * 32 + 8 * g + 4 * hh;
-          u32x2 w;
-          w.x = IO::pack2(o_acc[qb][dt][4 * g + 0] * inv_l, o_acc[qb][dt][4 * g + 1] * inv_l);
-          w.y = IO::pack2(o_acc[qb][dt][4 * g + 2] * inv_l, o_acc[qb][dt][4 * g + 3] * inv_l);
-          *(u32x2*)(orow + 2 * d) = w;
-        }
-    }
+      for (int g = 0; g < 4; ++g) {
+        const int d = dt * 32 + 8 * g + 4 * hh;
+        u32x2 w;
+        w.x = IO::pack2(o_acc[dt][4 * g + 0] * inv_l, o_acc[dt][4 * g + 1] * inv_l);
+        w.y = IO::pack2(o_acc[dt][4 * g + 2] * inv_l, o_acc[dt][4 * g + 3] * inv_l);
+        *(u32x2*)(orow + 2 * d) = w;
+      }
   }
 }
 
@@ -351,7 +388,7 @@ hipError_t run(const AttnDesc& d, hipStream_t s) {
   if (span >= (1ll << 31)) return hipErrorNotSupported;
   const int64_t blocks = (int64_t)d.B * d.H * p.qtiles;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_fwd<T, D>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_fwd<T, D>), dim3((unsigned)blocks), dim3(64 * kNW), 0, s, p);
   return hipGetLastError();
 }
 
