@@ -272,6 +272,13 @@ class Blas:
         return self.L.grxblasSgemm(self.h, int(ta), int(tb), m, n, k, fptr(alpha), A, lda, B, ldb,
                                    fptr(beta), C, ldc)
 
+    def set_cycle_probe(self, slots, capacity: int) -> int:
+        """Attach (or with slots=None detach) a device array of CycleSlot."""
+        return self.L.grxblasSetCycleProbe(self.h, slots, capacity)
+
+    def cycle_slots_needed(self, m: int, n: int) -> int:
+        return self.L.grxblasCycleSlotsNeeded(self.h, m, n)
+
     def sgemm_strided_batched(self, ta, tb, m, n, k, alpha, A, lda, sa, B, ldb, sb, beta, C, ldc, sc,
                               batch) -> int:
         return self.L.grxblasSgemmStridedBatched(self.h, int(ta), int(tb), m, n, k, fptr(alpha), A, lda,

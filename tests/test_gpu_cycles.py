@@ -1,0 +1,126 @@
+"""grxblasSetCycleProbe on gfx950: one grxCycleSlot per wave.
+
+Mirrors the reference's own use of the probe (ref tests/bench/gemm_cycles.cpp):
+slots sized by grxblasCycleSlotsNeeded(h, m, n), zeroed, attached, one call,
+detached, read back, on the same small shapes with all-ones inputs. On gfx950
+every wave of the GEMM kernels writes slot blockIdx*4 + wave: s_memtime at
+entry and at exit, core = XCD << 16 | CU id, warp = wave in its workgroup. A
+capacity below what the launch needs is refused before any launch (ref
+src/libs/grxblas/grxblas.cpp:690-692, 929-932).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import grxcp_amd as g
+from helpers import say, to_dev
+
+pytestmark = pytest.mark.gpu
+
+SLOT = ctypes.sizeof(g.CycleSlot)
+SLOT_DTYPE = np.dtype([("start", "<u8"), ("end", "<u8"), ("core", "<u4"), ("warp", "<u4")])
+F16_ONE, BF16_ONE = 0x3C00, 0x3F80
+GEMM_CYCLES_SHAPES = [(16, 16, 16), (16, 16, 32), (16, 16, 64), (32, 32, 32), (32, 32, 64)]
+
+
+def probe_call(blas, nslots, call):
+    buf = g.DeviceBuffer(nslots * SLOT)
+    buf.memset(0)
+    assert blas.set_cycle_probe(buf.p, nslots) == g.SUCCESS
+    status = call()
+    g.synchronize()
+    assert blas.set_cycle_probe(None, 0) == g.SUCCESS
+    raw = buf.download(np.uint8, nslots * SLOT)
+    return status, np.frombuffer(raw.tobytes(), dtype=SLOT_DTYPE)
+
+
+def check_written(slots, expected):
+    written = np.nonzero((slots["start"] != 0) | (slots["end"] != 0))[0]
+    assert written.tolist() == list(expected)
+    w = slots[written]
+    assert np.all(w["end"] > w["start"])
+    assert np.all(w["end"] - w["start"] < 10**9)
+    assert np.all((w["core"] >> 16) < 8), "XCD id"
+    assert np.all(w["warp"] == written % 4)
+    return w
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_CYCLES_SHAPES)
+def test_probe_gemm_ex_f16(blas, m, n, k):
+    nslots = blas.cycle_slots_needed(m, n)
+    assert nslots == 4
+    dA = to_dev(np.full(m * k, F16_ONE, np.uint16))
+    dB = to_dev(np.full(k * n, F16_ONE, np.uint16))
+    dC = to_dev(np.zeros(m * n, np.float32))
+    say(f"probe GemmEx f16 NN {m}x{n}x{k}")
+    s, slots = probe_call(blas, nslots, lambda: blas.gemm_ex(
+        0, 0, m, n, k, 1.0, dA.p, g.GRX_R_16F, m, dB.p, g.GRX_R_16F, k, 0.0, dC.p, g.GRX_R_32F, m))
+    assert s == g.SUCCESS, g.STATUS[s]
+    assert np.all(dC.download(np.float32, m * n) == k)
+    w = check_written(slots, range(4))
+    assert len(set(w["core"].tolist())) == 1, "one workgroup runs on one CU"
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_CYCLES_SHAPES)
+def test_probe_sgemm(blas, m, n, k):
+    nslots = blas.cycle_slots_needed(m, n)
+    dA = to_dev(np.ones(m * k, np.float32))
+    dB = to_dev(np.ones(k * n, np.float32))
+    dC = to_dev(np.zeros(m * n, np.float32))
+    say(f"probe Sgemm NN {m}x{n}x{k}")
+    s, slots = probe_call(blas, nslots, lambda: blas.sgemm(
+        0, 0, m, n, k, 1.0, dA.p, m, dB.p, k, 0.0, dC.p, m))
+    assert s == g.SUCCESS, g.STATUS[s]
+    assert np.all(dC.download(np.float32, m * n) == k)
+    w = check_written(slots, range(4))
+    assert len(set(w["core"].tolist())) == 1
+
+
+def test_probe_fast_path_bf16(blas):
+    m = n = k = 512  # TN, 16-byte rows: the 256x256-tile kernel, 4 workgroups
+    nslots = blas.cycle_slots_needed(m, n)
+    assert nslots == 4 * 8 * 8
+    dA = to_dev(np.full(m * k, BF16_ONE, np.uint16))
+    dB = to_dev(np.full(k * n, BF16_ONE, np.uint16))
+    dC = to_dev(np.zeros(m * n, np.uint16))
+    say("probe GemmEx bf16 TN 512^3 (fast path)")
+    s, slots = probe_call(blas, nslots, lambda: blas.gemm_ex(
+        1, 0, m, n, k, 1.0, dA.p, g.GRX_R_16BF, k, dB.p, g.GRX_R_16BF, k, 0.0, dC.p, g.GRX_R_16BF, m))
+    assert s == g.SUCCESS, g.STATUS[s]
+    assert np.all(dC.download(np.uint16, m * n) == 0x4400)  # bf16(512)
+    check_written(slots, range(16))
+
+
+def test_probe_batched_sgemm_needs_slots_per_member(blas):
+    m = n = k = 16
+    batch = 3
+    need = blas.cycle_slots_needed(m, n) * batch
+    dA = to_dev(np.ones(m * k * batch, np.float32))
+    dB = to_dev(np.ones(k * n * batch, np.float32))
+    dC = to_dev(np.zeros(m * n * batch, np.float32))
+    call = lambda: blas.sgemm_strided_batched(0, 0, m, n, k, 1.0, dA.p, m, m * k, dB.p, k, k * n,
+                                              0.0, dC.p, m, m * n, batch)
+    say("probe SgemmStridedBatched 16^3 x3, one slot short")
+    s, slots = probe_call(blas, need - 1, call)
+    assert s == g.INVALID_VALUE
+    assert not np.any(slots["end"])
+    assert np.all(dC.download(np.float32, m * n * batch) == 0), "refused before any launch"
+    say("probe SgemmStridedBatched 16^3 x3")
+    s, slots = probe_call(blas, need, call)
+    assert s == g.SUCCESS, g.STATUS[s]
+    assert np.all(dC.download(np.float32, m * n * batch) == k)
+    check_written(slots, range(need))
+
+
+def test_probe_capacity_refused_for_gemm_ex(blas):
+    m = n = k = 32
+    dA = to_dev(np.full(m * k, F16_ONE, np.uint16))
+    dB = to_dev(np.full(k * n, F16_ONE, np.uint16))
+    dC = to_dev(np.full(m * n, 7.0, np.float32))
+    say("probe GemmEx with too few slots")
+    s, slots = probe_call(blas, blas.cycle_slots_needed(m, n) - 1, lambda: blas.gemm_ex(
+        0, 0, m, n, k, 1.0, dA.p, g.GRX_R_16F, m, dB.p, g.GRX_R_16F, k, 0.0, dC.p, g.GRX_R_32F, m))
+    assert s == g.INVALID_VALUE
+    assert np.all(dC.download(np.float32, m * n) == 7.0)
+    assert not np.any(slots["end"])
