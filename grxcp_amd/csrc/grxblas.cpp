@@ -370,7 +370,10 @@ grxblasStatus_t grxblasSaxpy(grxblasHandle_t handle, int n, const float* alpha, 
   if (incx == 0 || incy == 0) return GRXBLAS_STATUS_INVALID_VALUE;
   const grxblasStatus_t s = ensure_ready(*handle);
   if (s != GRXBLAS_STATUS_SUCCESS) return s;
-  return from_hip(grxk::launch_saxpy(n, *alpha, x, incx, y, incy, handle->stream));
+  grxCycleSlot* probe = nullptr;
+  const grxblasStatus_t ps = probe_for(*handle, 4 * grxk::l1_blocks(n), &probe);
+  if (ps != GRXBLAS_STATUS_SUCCESS) return ps;
+  return from_hip(grxk::launch_saxpy(n, *alpha, x, incx, y, incy, probe, handle->stream));
 }
 
 grxblasStatus_t grxblasSscal(grxblasHandle_t handle, int n, const float* alpha, float* x,
@@ -383,7 +386,10 @@ grxblasStatus_t grxblasSscal(grxblasHandle_t handle, int n, const float* alpha, 
   if (incx <= 0) return GRXBLAS_STATUS_INVALID_VALUE;
   const grxblasStatus_t s = ensure_ready(*handle);
   if (s != GRXBLAS_STATUS_SUCCESS) return s;
-  return from_hip(grxk::launch_sscal(n, *alpha, x, incx, handle->stream));
+  grxCycleSlot* probe = nullptr;
+  const grxblasStatus_t ps = probe_for(*handle, 4 * grxk::l1_blocks(n), &probe);
+  if (ps != GRXBLAS_STATUS_SUCCESS) return ps;
+  return from_hip(grxk::launch_sscal(n, *alpha, x, incx, probe, handle->stream));
 }
 
 grxblasStatus_t grxblasSgemv(grxblasHandle_t handle, grxblasOperation_t trans, int m, int n,
@@ -398,8 +404,12 @@ grxblasStatus_t grxblasSgemv(grxblasHandle_t handle, grxblasOperation_t trans, i
   if (lda < m) return GRXBLAS_STATUS_INVALID_VALUE;
   const grxblasStatus_t s = ensure_ready(*handle);
   if (s != GRXBLAS_STATUS_SUCCESS) return s;
+  grxCycleSlot* probe = nullptr;
+  const grxblasStatus_t ps =
+      probe_for(*handle, 4 * grxk::sgemv_blocks(trans == GRXBLAS_OP_T, m, n), &probe);
+  if (ps != GRXBLAS_STATUS_SUCCESS) return ps;
   return from_hip(grxk::launch_sgemv(trans == GRXBLAS_OP_T, m, n, *alpha, (const float*)A, lda,
-                                     (const float*)x, incx, *beta, (float*)y, incy,
+                                     (const float*)x, incx, *beta, (float*)y, incy, probe,
                                      handle->stream));
 }
 

@@ -116,37 +116,53 @@ __device__ __forceinline__ int64_t blas_index(int i, int n, int inc) {
   return inc > 0 ? (int64_t)i * inc : (int64_t)(n - 1 - i) * (int64_t)(-inc);
 }
 
-__global__ void saxpy_kernel(int n, float alpha, const float* x, int incx, float* y, int incy) {
+// Level-1/2 kernels run 256-thread workgroups; with a cycle probe attached
+// every wave writes slot blockIdx*4 + wave, like the GEMM kernels.
+__device__ __forceinline__ void l12_record(grxCycleSlot* probe, uint64_t t0) {
+  cycle_record(probe, t0, blockIdx.x * 4 + (threadIdx.x >> 6), threadIdx.x >> 6);
+}
+
+__global__ void saxpy_kernel(int n, float alpha, const float* x, int incx, float* y, int incy,
+                             grxCycleSlot* probe) {
+  const uint64_t t0 = probe ? cycle_now() : 0;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
     const int64_t xi = blas_index((int)i, n, incx), yi = blas_index((int)i, n, incy);
     y[yi] = fmaf(alpha, x[xi], y[yi]);
   }
+  l12_record(probe, t0);
 }
 
-__global__ void sscal_kernel(int n, float alpha, float* x, int incx) {
+__global__ void sscal_kernel(int n, float alpha, float* x, int incx, grxCycleSlot* probe) {
+  const uint64_t t0 = probe ? cycle_now() : 0;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     x[(int64_t)i * incx] *= alpha;
+  l12_record(probe, t0);
 }
 
 // y = alpha*A*x + beta*y (A m x n col-major): one thread per output row; the
 // column walk keeps lanes on consecutive rows of A, so each step coalesces.
 __global__ void sgemv_n_kernel(int m, int n, float alpha, const float* A, int lda,
-                               const float* x, int incx, float beta, float* y, int incy) {
+                               const float* x, int incx, float beta, float* y, int incy,
+                               grxCycleSlot* probe) {
+  const uint64_t t0 = probe ? cycle_now() : 0;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= m) return;
-  float acc = 0.0f;
-  for (int j = 0; j < n; ++j) acc = fmaf(A[(int64_t)j * lda + i], x[blas_index(j, n, incx)], acc);
-  const int64_t yi = blas_index(i, m, incy);
-  y[yi] = (beta == 0.0f) ? alpha * acc : fmaf(beta, y[yi], alpha * acc);
+  if (i < m) {
+    float acc = 0.0f;
+    for (int j = 0; j < n; ++j) acc = fmaf(A[(int64_t)j * lda + i], x[blas_index(j, n, incx)], acc);
+    const int64_t yi = blas_index(i, m, incy);
+    y[yi] = (beta == 0.0f) ? alpha * acc : fmaf(beta, y[yi], alpha * acc);
+  }
+  l12_record(probe, t0);
 }
 
 // y = alpha*A^T*x + beta*y: one 256-thread workgroup per output, the lanes
 // stride down a column of A together and reduce in LDS.
 __global__ __launch_bounds__(256) void sgemv_t_kernel(int m, int n, float alpha, const float* A,
                                                       int lda, const float* x, int incx, float beta,
-                                                      float* y, int incy) {
+                                                      float* y, int incy, grxCycleSlot* probe) {
+  const uint64_t t0 = probe ? cycle_now() : 0;
   __shared__ float part[4];
   const int j = blockIdx.x;
   float acc = 0.0f;
@@ -160,6 +176,7 @@ __global__ __launch_bounds__(256) void sgemv_t_kernel(int m, int n, float alpha,
     const int64_t yi = blas_index(j, n, incy);
     y[yi] = (beta == 0.0f) ? alpha * t : fmaf(beta, y[yi], alpha * t);
   }
+  l12_record(probe, t0);
 }
 
 }  // namespace
@@ -180,27 +197,34 @@ hipError_t launch_sgemm(const SgemmDesc& d, hipStream_t s) {
   return hipGetLastError();
 }
 
+int64_t l1_blocks(int n) { return std::min<int64_t>(((int64_t)n + 255) / 256, 65536); }
+
+int64_t sgemv_blocks(bool trans, int m, int n) { return trans ? n : ((int64_t)m + 255) / 256; }
+
 hipError_t launch_saxpy(int n, float alpha, const float* x, int incx, float* y, int incy,
-                        hipStream_t s) {
-  const int blocks = (int)std::min<int64_t>(((int64_t)n + 255) / 256, 65536);
-  hipLaunchKernelGGL(saxpy_kernel, dim3(blocks), dim3(256), 0, s, n, alpha, x, incx, y, incy);
+                        grxCycleSlot* probe, hipStream_t s) {
+  hipLaunchKernelGGL(saxpy_kernel, dim3((unsigned)l1_blocks(n)), dim3(256), 0, s, n, alpha, x, incx,
+                     y, incy, probe);
   return hipGetLastError();
 }
 
-hipError_t launch_sscal(int n, float alpha, float* x, int incx, hipStream_t s) {
-  const int blocks = (int)std::min<int64_t>(((int64_t)n + 255) / 256, 65536);
-  hipLaunchKernelGGL(sscal_kernel, dim3(blocks), dim3(256), 0, s, n, alpha, x, incx);
+hipError_t launch_sscal(int n, float alpha, float* x, int incx, grxCycleSlot* probe,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(sscal_kernel, dim3((unsigned)l1_blocks(n)), dim3(256), 0, s, n, alpha, x, incx,
+                     probe);
   return hipGetLastError();
 }
 
 hipError_t launch_sgemv(bool trans, int m, int n, float alpha, const float* A, int lda,
-                        const float* x, int incx, float beta, float* y, int incy, hipStream_t s) {
+                        const float* x, int incx, float beta, float* y, int incy,
+                        grxCycleSlot* probe, hipStream_t s) {
+  const unsigned blocks = (unsigned)sgemv_blocks(trans, m, n);
   if (!trans) {
-    hipLaunchKernelGGL(sgemv_n_kernel, dim3((m + 255) / 256), dim3(256), 0, s, m, n, alpha, A, lda,
-                       x, incx, beta, y, incy);
+    hipLaunchKernelGGL(sgemv_n_kernel, dim3(blocks), dim3(256), 0, s, m, n, alpha, A, lda, x, incx,
+                       beta, y, incy, probe);
   } else {
-    hipLaunchKernelGGL(sgemv_t_kernel, dim3(n), dim3(256), 0, s, m, n, alpha, A, lda, x, incx,
-                       beta, y, incy);
+    hipLaunchKernelGGL(sgemv_t_kernel, dim3(blocks), dim3(256), 0, s, m, n, alpha, A, lda, x, incx,
+                       beta, y, incy, probe);
   }
   return hipGetLastError();
 }

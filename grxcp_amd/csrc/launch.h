@@ -49,13 +49,16 @@ struct SgemmDesc {
 };
 hipError_t launch_sgemm(const SgemmDesc& d, hipStream_t s);
 
-// Level 1/2, fp32.
+// Level 1/2, fp32 (256-thread workgroups; with a probe, 4 slots per workgroup).
+int64_t l1_blocks(int n);
+int64_t sgemv_blocks(bool trans, int m, int n);
 hipError_t launch_saxpy(int n, float alpha, const float* x, int incx, float* y,
-                        int incy, hipStream_t s);
-hipError_t launch_sscal(int n, float alpha, float* x, int incx, hipStream_t s);
+                        int incy, grxCycleSlot* probe, hipStream_t s);
+hipError_t launch_sscal(int n, float alpha, float* x, int incx, grxCycleSlot* probe,
+                        hipStream_t s);
 hipError_t launch_sgemv(bool trans, int m, int n, float alpha, const float* A,
                         int lda, const float* x, int incx, float beta, float* y,
-                        int incy, hipStream_t s);
+                        int incy, grxCycleSlot* probe, hipStream_t s);
 
 // grxDNN.
 enum class NormType { BF16, F16, F32 };

@@ -124,3 +124,36 @@ def test_probe_capacity_refused_for_gemm_ex(blas):
     assert s == g.INVALID_VALUE
     assert np.all(dC.download(np.float32, m * n) == 7.0)
     assert not np.any(slots["end"])
+
+
+def test_probe_level12(blas):
+    """Level 1/2 calls write one slot per wave of their 256-thread workgroups
+    (the reference writes one per block there, ref grxblas.cpp:764-766)."""
+    n = 1000  # saxpy / sscal: 4 workgroups
+    dx = to_dev(np.arange(n, dtype=np.float32))
+    dy = to_dev(np.ones(n, np.float32))
+    say("probe saxpy n=1000, one slot short")
+    s, slots = probe_call(blas, 15, lambda: blas.L.grxblasSaxpy(blas.h, n, g.fptr(2.0), dx.p, 1, dy.p, 1))
+    assert s == g.INVALID_VALUE and not np.any(slots["end"])
+    assert np.all(dy.download(np.float32, n) == 1.0)
+    say("probe saxpy n=1000")
+    s, slots = probe_call(blas, 16, lambda: blas.L.grxblasSaxpy(blas.h, n, g.fptr(2.0), dx.p, 1, dy.p, 1))
+    assert s == g.SUCCESS
+    assert np.array_equal(dy.download(np.float32, n), 2.0 * np.arange(n, dtype=np.float32) + 1.0)
+    check_written(slots, range(16))
+    say("probe sscal n=1000")
+    s, slots = probe_call(blas, 16, lambda: blas.L.grxblasSscal(blas.h, n, g.fptr(0.5), dx.p, 1))
+    assert s == g.SUCCESS
+    check_written(slots, range(16))
+    m, nn = 300, 5
+    dA = to_dev(np.ones(m * nn, np.float32))
+    dv = to_dev(np.ones(max(m, nn), np.float32))
+    dw = to_dev(np.zeros(max(m, nn), np.float32))
+    for trans, blocks in ((0, 2), (1, nn)):
+        say(f"probe sgemv trans={trans} {m}x{nn}")
+        s, slots = probe_call(blas, 4 * blocks, lambda: blas.L.grxblasSgemv(
+            blas.h, trans, m, nn, g.fptr(1.0), dA.p, m, dv.p, 1, g.fptr(0.0), dw.p, 1))
+        assert s == g.SUCCESS
+        out = dw.download(np.float32, nn if trans else m)
+        assert np.all(out == (m if trans else nn))
+        check_written(slots, range(4 * blocks))
