@@ -32,7 +32,7 @@ sys.path.insert(0, ROOT)
 import grxcp_amd as g  # noqa: E402
 from grxcp_amd import synth  # noqa: E402
 
-PEAK = {"bf16": 2500.0, "int8": 5000.0, "hbm": 8000.0}  # TFLOP/s, TOP/s, GB/s (MI355X dense)
+PEAK = {"bf16": 2500.0, "int8": 5000.0, "fp32": 157.3, "hbm": 8000.0}  # TFLOP/s, TOP/s, GB/s (MI355X dense)
 BF16, I8, I32 = g.GRX_R_16BF, g.GRX_R_8I, g.GRX_R_32I
 
 
@@ -77,7 +77,7 @@ def roofline(bound: str, work: float, ms: float, peak_key: str, traffic_key: str
         unit = "GB/s"
     else:
         achieved = work / (ms * 1e-3) / 1e12     # TFLOP/s (TOP/s for int8)
-        unit = "TFLOP/s" if peak_key == "bf16" else "TOP/s"
+        unit = "TOP/s" if peak_key == "int8" else "TFLOP/s"
     peak = PEAK[peak_key]
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(traffic_key)}
@@ -189,6 +189,29 @@ def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu):
     return out
 
 
+def bench_sgemm(stream, blas, steps, warmup):
+    """grxblasSgemm fp32 4096^3 (N, N, column-major), fp32 matrix-core roofline."""
+    M = N = K = 4096
+    log("Sgemm 4096^3: generating inputs")
+    A = synth.uniform_f32(M * K, 41, -1.0, 1.0)
+    B = synth.uniform_f32(K * N, 42, -1.0, 1.0)
+    dA, dB, dC = g.DeviceBuffer.from_array(A), g.DeviceBuffer.from_array(B), g.DeviceBuffer(M * N * 4)
+    one, zero = g.fptr(1.0), g.fptr(0.0)
+
+    def launch():
+        s = blas.L.grxblasSgemm(blas.h, 0, 0, M, N, K, one, dA.p, M, dB.p, K, zero, dC.p, M)
+        if s:
+            raise g.GrxError(f"Sgemm status {s}")
+    log("Sgemm 4096^3: timing")
+    ms = time_launches(stream, launch, steps, warmup)
+    flops = 2.0 * M * N * K
+    out = {"name": "sgemm_fp32_4096", "ms": round(ms, 4), "value": round(flops / ms / 1e9, 2),
+           "unit": "TFLOP/s", "roofline": roofline("mfma", flops, ms, "fp32", "sgemm_fp32_4096")}
+    for d in (dA, dB, dC):
+        d.close()
+    return out
+
+
 def bench_gemm_int8(stream, blas, steps, warmup, cpu):
     M, K, N = 4096, 8192, 28672
     log("int8 GEMM + dequant: generating inputs")
@@ -288,7 +311,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention")
+    ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention,sgemm")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy kernel of MIB MiB (torch), "
                          "the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -333,6 +356,8 @@ def main() -> int:
         ops.append(bench_norm(stream, dnn, True, args.steps, args.warmup, cpu))
     if want("attention"):
         ops.append(bench_attention(stream, dnn, args.steps, args.warmup, cpu))
+    if want("sgemm"):
+        ops.append(bench_sgemm(stream, blas, args.steps, args.warmup))
 
     if headline is None:
         headline = ops.pop(0)

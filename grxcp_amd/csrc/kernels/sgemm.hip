@@ -3,8 +3,9 @@
 //
 // Sgemm replaces the reference's one-thread-per-output kernel
 // (ref: src/libs/grxblas/kernels/sgemm.cpp:22-89; 2 global loads per
-// multiply-add) with an LDS-tiled kernel: a 64x64 tile of C per 256-thread
-// workgroup, 4x4 outputs per thread, 16-deep K stages staged through LDS with
+// multiply-add) with an fp32 matrix-core kernel (v_mfma_f32_32x32x2_f32): a
+// 128x128 (or, for problems too small to fill the chip, 64x64) tile of C per
+// 256-thread workgroup, 16-deep K stages double-buffered through LDS with
 // guarded loads that apply op() while staging (all four transposes, ragged
 // shapes, any leading dimension). The batch is the grid's z dimension with
 // signed element strides (a zero stride broadcasts an operand), exactly the
@@ -20,7 +21,6 @@
 namespace grxk {
 namespace {
 
-constexpr int kT = 64;   // C tile edge
 constexpr int kK = 16;   // K per stage
 
 struct SParams {
@@ -34,82 +34,137 @@ struct SParams {
   grxCycleSlot* probe;
 };
 
-__global__ __launch_bounds__(256) void sgemm_tiled(SParams p) {
-  __shared__ float As[kK][kT + 4];   // As[kk][i] = op(A)[row0+i][k0+kk]
-  __shared__ float Bs[kK][kT + 4];   // Bs[kk][j] = op(B)[k0+kk][col0+j]
+// One workgroup = 4 waves (2 x 2) computes an MT x MT tile of C with
+// v_mfma_f32_32x32x2_f32 (each wave MT/2 x MT/2, i.e. (MT/64)^2 .. 4 MFMA
+// tiles). K advances 16 at a time through double-buffered LDS tiles
+// As[kk][i] = op(A)[row0+i][k0+kk] and Bs[kk][j] = op(B)[k0+kk][col0+j]; the
+// next stage's guarded loads (op() applied while loading, zeros outside the
+// matrix) are issued before the current stage's MFMAs and stored after them,
+// one barrier per stage. An MFMA k-step reads one float per lane per operand:
+// lane l takes row/column l%32 at k = 2s + l/32.
+// VEC: leading dimensions, strides and base pointers are multiples of 4
+// floats, so 4 consecutive elements along an operand's contiguous dimension
+// are one aligned 16-byte load (groups that cross the matrix edge fall back
+// to guarded scalar loads).
+template <int MT, bool VEC>
+__global__ __launch_bounds__(256) void sgemm_mfma(SParams p) {
+  constexpr int WT = MT / 2;            // wave tile edge
+  constexpr int NF = WT / 32;           // 32x32 MFMA tiles per wave edge
+  constexpr int PITCH = MT + 4;         // rows of 16 consecutive k land in distinct banks
+  constexpr int PER = MT * kK / 256;    // elements per thread per operand per stage
+  __shared__ float As[2][kK][PITCH];
+  __shared__ float Bs[2][kK][PITCH];
 
   const uint64_t t0 = p.probe ? cycle_now() : 0;
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
   const int tm = blockIdx.x % p.tiles_m;
   const int tn = blockIdx.x / p.tiles_m;
-  const int row0 = tm * kT, col0 = tn * kT;
+  const int row0 = tm * MT, col0 = tn * MT;
   const int64_t bz = blockIdx.z;
   const float* A = p.a + bz * p.sa;
   const float* B = p.b + bz * p.sb;
   float* C = p.c + bz * p.sc;
 
-  // Thread (ti, tj) owns rows ti + 16*r and columns tj + 16*c: consecutive
-  // lanes own consecutive rows, so C stores coalesce along its columns.
-  const int ti = tid & 15, tj = tid >> 4;
-  float acc[4][4];
+  // Staging: an operand stage is MT x 16 elements read along its storage's
+  // contiguous dimension (op(A): i for N, k for T; op(B): k for N, j for T)
+  // in groups of 4 consecutive elements; thread t handles groups
+  // t + 256*q. Element (cont, other) of a group maps to LDS [kk][i or j].
+  constexpr int GPT = PER / 4;  // groups per thread per operand
+  float ra[PER], rb[PER];
+  auto load_group = [&](const float* X, int64_t ld, bool kcont, int lim_cont, int lim_other,
+                        int cont, int other, float* out) {
+    // element (c, o): X[o*ld + c] in storage; valid iff c < lim_cont, o < lim_other
+    const float* q = X + (int64_t)other * ld + cont;
+    if (VEC && other < lim_other && cont + 3 < lim_cont) {
+      const float4 v = *(const float4*)q;
+      out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+    } else {
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+      for (int v = 0; v < 4; ++v) out[v] = (other < lim_other && cont + v < lim_cont) ? q[v] : 0.0f;
+    }
+    (void)kcont;
+  };
+  // op(A) (m x k): N stores A[k*lda + i] (cont = i), T stores A[i*lda + k] (cont = k).
+  // op(B) (k x n): N stores B[j*ldb + k] (cont = k), T stores B[k*ldb + j] (cont = j).
+  auto load = [&](int k0) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[r][c] = 0.0f;
+    for (int q = 0; q < GPT; ++q) {
+      const int e = 4 * (tid + 256 * q);
+      if (p.ta) load_group(A, p.lda, true, p.k, p.m, k0 + e % kK, row0 + e / kK, &ra[4 * q]);
+      else load_group(A, p.lda, false, p.m, p.k, row0 + e % MT, k0 + e / MT, &ra[4 * q]);
+      if (p.tb) load_group(B, p.ldb, false, p.n, p.k, col0 + e % MT, k0 + e / MT, &rb[4 * q]);
+      else load_group(B, p.ldb, true, p.k, p.n, k0 + e % kK, col0 + e / kK, &rb[4 * q]);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < GPT; ++q) {
+      const int e = 4 * (tid + 256 * q);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (p.ta) As[buf][e % kK + v][e / kK] = ra[4 * q + v];
+        else As[buf][e / MT][e % MT + v] = ra[4 * q + v];
+        if (p.tb) Bs[buf][e / MT][e % MT + v] = rb[4 * q + v];
+        else Bs[buf][e % kK + v][e / kK] = rb[4 * q + v];
+      }
+    }
+  };
 
+  f32x16 acc[NF][NF];
+#pragma unroll
+  for (int fm = 0; fm < NF; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < NF; ++fn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+  load(0);
+  store(0);
+  __syncthreads();
+  int buf = 0;
   for (int k0 = 0; k0 < p.k; k0 += kK) {
+    const bool more = k0 + kK < p.k;
+    if (more) load(k0 + kK);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = tid + 256 * q;   // 1024 elements per operand stage
-      // op(A): stored m x k (N, contiguous in i) or k x m (T, contiguous in k)
-      int i, kk;
-      if (p.ta) { kk = e % kK; i = e / kK; } else { i = e % kT; kk = e / kT; }
-      const int gi = row0 + i, gk = k0 + kk;
-      float va = 0.0f;
-      if (gi < p.m && gk < p.k)
-        va = p.ta ? A[(int64_t)gi * p.lda + gk] : A[(int64_t)gk * p.lda + gi];
-      As[kk][i] = va;
-      // op(B): stored k x n (N, contiguous in k) or n x k (T, contiguous in j)
-      int j;
-      if (!p.tb) { kk = e % kK; j = e / kK; } else { j = e % kT; kk = e / kT; }
-      const int gj = col0 + j;
-      const int gk2 = k0 + kk;
-      float vb = 0.0f;
-      if (gj < p.n && gk2 < p.k)
-        vb = p.tb ? B[(int64_t)gk2 * p.ldb + gj] : B[(int64_t)gj * p.ldb + gk2];
-      Bs[kk][j] = vb;
+    for (int s = 0; s < kK / 2; ++s) {
+      float av[NF], bv[NF];
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        av[f] = As[buf][2 * s + hh][WT * wm + 32 * f + l32];
+        bv[f] = Bs[buf][2 * s + hh][WT * wn + 32 * f + l32];
+      }
+#pragma unroll
+      for (int fm = 0; fm < NF; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < NF; ++fn)
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[fm], bv[fn], acc[fm][fn], 0, 0, 0);
     }
+    if (more) store(buf ^ 1);
     __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < kK; ++kk) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) av[r] = As[kk][ti + 16 * r];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) bv[c] = Bs[kk][tj + 16 * c];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(av[r], bv[c], acc[r][c]);
-    }
-    __syncthreads();
+    buf ^= 1;
   }
 
+  // C = alpha*acc + beta*C (col-major); lane holds column l32 of each MFMA
+  // tile and rows 8*(r/4) + 4*hh + r%4.
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int gj = col0 + tj + 16 * c;
-    if (gj >= p.n) continue;
+  for (int fm = 0; fm < NF; ++fm)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int gi = row0 + ti + 16 * r;
-      if (gi >= p.m) continue;
-      float* cp = C + (int64_t)gj * p.ldc + gi;
-      const float s = __fmul_rn(p.alpha, acc[r][c]);
-      *cp = (p.beta == 0.0f) ? s : __fadd_rn(s, __fmul_rn(p.beta, *cp));
+    for (int fn = 0; fn < NF; ++fn) {
+      const int gj = col0 + WT * wn + 32 * fn + l32;
+      if (gj >= p.n) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gi = row0 + WT * wm + 32 * fm + 8 * (r >> 2) + 4 * hh + (r & 3);
+        if (gi >= p.m) continue;
+        float* cp = C + (int64_t)gj * p.ldc + gi;
+        const float v = __fmul_rn(p.alpha, acc[fm][fn][r]);
+        *cp = (p.beta == 0.0f) ? v : __fadd_rn(v, __fmul_rn(p.beta, *cp));
+      }
     }
-  }
-  cycle_record(p.probe, t0,
-               (uint32_t)((bz * gridDim.x + blockIdx.x) * 4 + (tid >> 6)), tid >> 6);
+  cycle_record(p.probe, t0, (uint32_t)((bz * gridDim.x + blockIdx.x) * 4 + wave), wave);
 }
 
 __device__ __forceinline__ int64_t blas_index(int i, int n, int inc) {
@@ -190,10 +245,20 @@ hipError_t launch_sgemm(const SgemmDesc& d, hipStream_t s) {
   p.ta = d.ta; p.tb = d.tb;
   p.alpha = d.alpha; p.beta = d.beta;
   p.probe = d.probe;
-  p.tiles_m = (d.m + kT - 1) / kT;
-  const int64_t tiles = (int64_t)p.tiles_m * ((d.n + kT - 1) / kT);
-  if (tiles > 0x7fffffff || d.batch > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sgemm_tiled, dim3((unsigned)tiles, 1, (unsigned)d.batch), dim3(256), 0, s, p);
+  if (d.batch > 65535) return hipErrorInvalidValue;
+  // 128-wide tiles once they fill the chip, 64-wide below that.
+  const int64_t big = ((int64_t)(d.m + 127) / 128) * ((d.n + 127) / 128) * d.batch;
+  const int mt = big >= 256 ? 128 : 64;
+  p.tiles_m = (d.m + mt - 1) / mt;
+  const int64_t tiles = (int64_t)p.tiles_m * ((d.n + mt - 1) / mt);
+  if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+  const bool vec = d.lda % 4 == 0 && d.ldb % 4 == 0 && d.stride_a % 4 == 0 && d.stride_b % 4 == 0 &&
+                   (uintptr_t)d.a % 16 == 0 && (uintptr_t)d.b % 16 == 0;
+  const dim3 grid((unsigned)tiles, 1, (unsigned)d.batch);
+  if (mt == 128 && vec) hipLaunchKernelGGL((sgemm_mfma<128, true>), grid, dim3(256), 0, s, p);
+  else if (mt == 128) hipLaunchKernelGGL((sgemm_mfma<128, false>), grid, dim3(256), 0, s, p);
+  else if (vec) hipLaunchKernelGGL((sgemm_mfma<64, true>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((sgemm_mfma<64, false>), grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
