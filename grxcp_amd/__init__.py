@@ -31,6 +31,7 @@ STATUS = {
     4: "ARCH_MISMATCH", 5: "EXECUTION_FAILED", 6: "NOT_SUPPORTED", 7: "INTERNAL_ERROR",
 }
 SUCCESS, NOT_INITIALIZED, ALLOC_FAILED, INVALID_VALUE = 0, 1, 2, 3
+GELU_ERF, GELU_TANH = 0, 1
 ARCH_MISMATCH, EXECUTION_FAILED, NOT_SUPPORTED, INTERNAL_ERROR = 4, 5, 6, 7
 TENSOR_FP16, TENSOR_TF32, TENSOR_FP8, TENSOR_FP4 = 0x01, 0x02, 0x04, 0x08
 TENSOR_INT8, TENSOR_INT4, TENSOR_BF16 = 0x10, 0x20, 0x40
@@ -127,6 +128,8 @@ _DNN = {
                                      c_void_p, c_void_p]),
     "grxdnnLayerNormForward": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_float, c_void_p, c_void_p]),
+    "grxdnnSoftmaxForward": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "grxdnnGeluForward": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "grxdnnCreateAttentionDescriptor": (c_int, [POINTER(c_void_p)]),
     "grxdnnDestroyAttentionDescriptor": (c_int, [c_void_p]),
     "grxdnnSetAttentionDescriptor": (c_int, [c_void_p, c_int, c_float]),
@@ -347,6 +350,12 @@ class Dnn:
 
     def attention(self, ad, qd, q, kd, k, vd, v, od, o) -> int:
         return self.L.grxdnnAttentionForward(self.h, ad.d, qd.d, q, kd.d, k, vd.d, v, od.d, o)
+
+    def softmax(self, xd, x, yd, y) -> int:
+        return self.L.grxdnnSoftmaxForward(self.h, xd.d, x, yd.d, y)
+
+    def gelu(self, mode: int, xd, x, yd, y) -> int:
+        return self.L.grxdnnGeluForward(self.h, mode, xd.d, x, yd.d, y)
 
 
 class Stream:

@@ -160,6 +160,47 @@ grxdnnStatus_t norm_common(grxdnnHandle_t handle, grxdnnTensorDescriptor_t xDesc
   return from_hip(e);
 }
 
+// Softmax / GELU: x and y of one type and shape, rows flattening to one
+// stride each, innermost stride 1.
+grxdnnStatus_t row_common(grxdnnHandle_t handle, grxdnnTensorDescriptor_t xDesc, const void* x,
+                          grxdnnTensorDescriptor_t yDesc, void* y, grxk::NormType* nt,
+                          grxk::RowDesc* d, bool* empty) {
+  *empty = false;
+  if (!handle) return GRXDNN_STATUS_NOT_INITIALIZED;
+  if (!xDesc || !yDesc || !xDesc->set || !yDesc->set) return GRXDNN_STATUS_INVALID_VALUE;
+  if (!same_shape(*xDesc, *yDesc)) return GRXDNN_STATUS_INVALID_VALUE;
+  if (xDesc->type != yDesc->type) return GRXDNN_STATUS_NOT_SUPPORTED;
+  switch (xDesc->type) {
+    case GRX_R_16BF: *nt = grxk::NormType::BF16; break;
+    case GRX_R_16F:  *nt = grxk::NormType::F16; break;
+    case GRX_R_32F:  *nt = grxk::NormType::F32; break;
+    default: return GRXDNN_STATUS_NOT_SUPPORTED;
+  }
+  for (int i = 0; i < xDesc->nb - 1; ++i)
+    if (xDesc->dims[i] == 0) {  // no rows: nothing to do
+      *empty = true;
+      return GRXDNN_STATUS_SUCCESS;
+    }
+  const int hidden = xDesc->dims[xDesc->nb - 1];
+  if (hidden <= 0) return GRXDNN_STATUS_INVALID_VALUE;
+  if (hidden > (1 << 24)) return GRXDNN_STATUS_NOT_SUPPORTED;
+  if (xDesc->strides[xDesc->nb - 1] != 1 || yDesc->strides[yDesc->nb - 1] != 1)
+    return GRXDNN_STATUS_NOT_SUPPORTED;
+  int64_t rows = 0, yrows = 0, xp = 0, yp = 0;
+  if (!row_layout(*xDesc, &rows, &xp) || !row_layout(*yDesc, &yrows, &yp))
+    return GRXDNN_STATUS_NOT_SUPPORTED;
+  if (!x || !y) return GRXDNN_STATUS_INVALID_VALUE;
+  const grxdnnStatus_t s = ensure_device(*handle);
+  if (s != GRXDNN_STATUS_SUCCESS) return s;
+  d->rows = rows;
+  d->hidden = hidden;
+  d->x_row_stride = xp;
+  d->y_row_stride = yp;
+  d->x = x;
+  d->y = y;
+  return GRXDNN_STATUS_SUCCESS;
+}
+
 }  // namespace
 
 extern "C" {
@@ -269,6 +310,29 @@ grxdnnStatus_t grxdnnLayerNormForward(grxdnnHandle_t handle, grxdnnTensorDescrip
                                       const void* gamma, const void* beta, float eps,
                                       grxdnnTensorDescriptor_t yDesc, void* y) {
   return norm_common(handle, xDesc, x, wDesc, gamma, beta, true, eps, yDesc, y);
+}
+
+grxdnnStatus_t grxdnnSoftmaxForward(grxdnnHandle_t handle, grxdnnTensorDescriptor_t xDesc,
+                                    const void* x, grxdnnTensorDescriptor_t yDesc, void* y) {
+  grxk::NormType nt{};
+  grxk::RowDesc d{};
+  bool empty = false;
+  const grxdnnStatus_t s = row_common(handle, xDesc, x, yDesc, y, &nt, &d, &empty);
+  if (s != GRXDNN_STATUS_SUCCESS || empty) return s;
+  return from_hip(grxk::launch_softmax(nt, d, handle->stream));
+}
+
+grxdnnStatus_t grxdnnGeluForward(grxdnnHandle_t handle, grxdnnGeluMode_t mode,
+                                 grxdnnTensorDescriptor_t xDesc, const void* x,
+                                 grxdnnTensorDescriptor_t yDesc, void* y) {
+  if (!handle) return GRXDNN_STATUS_NOT_INITIALIZED;
+  if (mode != GRXDNN_GELU_ERF && mode != GRXDNN_GELU_TANH) return GRXDNN_STATUS_INVALID_VALUE;
+  grxk::NormType nt{};
+  grxk::RowDesc d{};
+  bool empty = false;
+  const grxdnnStatus_t s = row_common(handle, xDesc, x, yDesc, y, &nt, &d, &empty);
+  if (s != GRXDNN_STATUS_SUCCESS || empty) return s;
+  return from_hip(grxk::launch_gelu(nt, mode == GRXDNN_GELU_TANH, d, handle->stream));
 }
 
 grxdnnStatus_t grxdnnCreateAttentionDescriptor(grxdnnAttentionDescriptor_t* d) {

@@ -1,0 +1,215 @@
+// grxDNN softmax (over the last dimension) and GELU forward on gfx950.
+//
+// New: the reference plans both for grxDNN (ref
+// docs/designs/grxcp_roadmap.md:864-877, grxcp_architecture.md:594) and ships
+// neither. Both are HBM-bound streams: x is read once and y written once.
+//
+// Softmax, rows of up to 1024 16-byte chunks: one row per wavefront, held
+// packed in registers; the row max and the sum of exp(x - max) are shuffle
+// reductions (no LDS, no barrier); y = exp(x - max) / sum in fp32, rounded
+// once. Longer or unaligned rows: one row per workgroup, three element-wise
+// passes (max, sum, write) re-reading x.
+// GELU: grid-stride over 16-byte chunks of every row (element-wise for
+// unaligned layouts), erf or tanh form in fp32, rounded once.
+
+#include "../launch.h"
+#include "device_common.h"
+#include "row_io.h"
+
+namespace grxk {
+namespace {
+
+struct RParams {
+  const uint8_t* x;
+  uint8_t* y;
+  int64_t x_rs, y_rs;  // row strides, elements
+  int64_t rows;
+  int hidden;
+};
+
+template <NormType T, int NC>
+__global__ __launch_bounds__(256) void softmax_wave(RParams p) {
+  using IO = Io<T>;
+  constexpr int V = IO::kVec;
+  const int lane = threadIdx.x & 63;
+  const int nchunks = p.hidden / V;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < p.rows; row += nwaves) {
+    const uint8_t* xrow = p.x + row * p.x_rs * (int64_t)(16 / V);
+    uint8_t* yrow = p.y + row * p.y_rs * (int64_t)(16 / V);
+    u32x4 raw[NC];
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+      const int c = lane + 64 * q;
+      raw[q] = c < nchunks ? __builtin_nontemporal_load((const u32x4*)xrow + c) : u32x4{0, 0, 0, 0};
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+      if (lane + 64 * q >= nchunks) continue;
+      float v[V];
+      IO::unpack(raw[q], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e) mx = fmaxf(mx, v[e]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+      if (lane + 64 * q >= nchunks) continue;
+      float v[V];
+      IO::unpack(raw[q], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e) sum += expf(v[e] - mx);
+    }
+    // Keep only the packed row live between passes.
+#pragma unroll
+    for (int q = 0; q < NC; ++q) asm volatile("" : "+v"(raw[q]));
+    const float inv = 1.0f / wave_sum(sum);
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+      const int c = lane + 64 * q;
+      if (c >= nchunks) continue;
+      float v[V], o[V];
+      IO::unpack(raw[q], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e) o[e] = expf(v[e] - mx) * inv;
+      __builtin_nontemporal_store(IO::pack(o), (u32x4*)yrow + c);
+    }
+  }
+}
+
+// Identical in every thread of the 256-thread workgroup.
+__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  __syncthreads();  // red[] may still be read from a previous reduction
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]))
+                : (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <NormType T>
+__global__ __launch_bounds__(256) void softmax_rows(RParams p) {
+  using IO = Io<T>;
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
+    const int64_t xo = row * p.x_rs, yo = row * p.y_rs;
+    float mx = -INFINITY;
+    for (int c = tid; c < p.hidden; c += 256) mx = fmaxf(mx, IO::ld(p.x, xo + c));
+    mx = block_reduce(mx, red, true);
+    float sum = 0.0f;
+    for (int c = tid; c < p.hidden; c += 256) sum += expf(IO::ld(p.x, xo + c) - mx);
+    const float inv = 1.0f / block_reduce(sum, red, false);
+    for (int c = tid; c < p.hidden; c += 256) IO::st(p.y, yo + c, expf(IO::ld(p.x, xo + c) - mx) * inv);
+  }
+}
+
+template <bool TANH> __device__ __forceinline__ float gelu(float x) {
+  if (TANH) {
+    const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+    return 0.5f * x * (1.0f + tanhf(k0 * (x + 0.044715f * x * x * x)));
+  }
+  return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
+}
+
+template <NormType T, bool TANH>
+__global__ __launch_bounds__(256) void gelu_vec(RParams p) {
+  using IO = Io<T>;
+  constexpr int V = IO::kVec;
+  const int nchunks = p.hidden / V;
+  const int64_t total = p.rows * nchunks;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    const int64_t row = i / nchunks;
+    const int c = (int)(i - row * nchunks);
+    const u32x4 w = __builtin_nontemporal_load(
+        (const u32x4*)(p.x + row * p.x_rs * (int64_t)(16 / V)) + c);
+    float v[V];
+    IO::unpack(w, v);
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = gelu<TANH>(v[e]);
+    __builtin_nontemporal_store(IO::pack(v), (u32x4*)(p.y + row * p.y_rs * (int64_t)(16 / V)) + c);
+  }
+}
+
+template <NormType T, bool TANH>
+__global__ __launch_bounds__(256) void gelu_scalar(RParams p) {
+  using IO = Io<T>;
+  const int64_t total = p.rows * p.hidden;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    const int64_t row = i / p.hidden;
+    const int c = (int)(i - row * p.hidden);
+    IO::st(p.y, row * p.y_rs + c, gelu<TANH>(IO::ld(p.x, row * p.x_rs + c)));
+  }
+}
+
+RParams make_params(const RowDesc& d) {
+  RParams p{};
+  p.x = (const uint8_t*)d.x;
+  p.y = (uint8_t*)d.y;
+  p.x_rs = d.x_row_stride;
+  p.y_rs = d.y_row_stride;
+  p.rows = d.rows;
+  p.hidden = d.hidden;
+  return p;
+}
+
+template <NormType T>
+bool vec_layout(const RowDesc& d) {
+  constexpr int V = Io<T>::kVec;
+  return d.hidden % V == 0 && d.x_row_stride % V == 0 && d.y_row_stride % V == 0 &&
+         (uintptr_t)d.x % 16 == 0 && (uintptr_t)d.y % 16 == 0;
+}
+
+template <NormType T>
+hipError_t run_softmax(const RowDesc& d, hipStream_t s) {
+  const RParams p = make_params(d);
+  const int nchunks = d.hidden / Io<T>::kVec;
+  const unsigned wgrid = (unsigned)std::min<int64_t>((d.rows + 3) / 4, 1 << 30);
+  const bool vec = vec_layout<T>(d);
+  if (vec && nchunks <= 64) hipLaunchKernelGGL((softmax_wave<T, 1>), dim3(wgrid), dim3(256), 0, s, p);
+  else if (vec && nchunks <= 128) hipLaunchKernelGGL((softmax_wave<T, 2>), dim3(wgrid), dim3(256), 0, s, p);
+  else if (vec && nchunks <= 256) hipLaunchKernelGGL((softmax_wave<T, 4>), dim3(wgrid), dim3(256), 0, s, p);
+  else if (vec && nchunks <= 512) hipLaunchKernelGGL((softmax_wave<T, 8>), dim3(wgrid), dim3(256), 0, s, p);
+  else if (vec && nchunks <= 1024) hipLaunchKernelGGL((softmax_wave<T, 16>), dim3(wgrid), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((softmax_rows<T>), dim3((unsigned)std::min<int64_t>(d.rows, 1 << 30)), dim3(256),
+                       0, s, p);
+  return hipGetLastError();
+}
+
+template <NormType T, bool TANH>
+hipError_t run_gelu(const RowDesc& d, hipStream_t s) {
+  const RParams p = make_params(d);
+  const bool vec = vec_layout<T>(d);
+  const int64_t items = vec ? d.rows * (d.hidden / Io<T>::kVec) : d.rows * d.hidden;
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((items + 255) / 256, 1 << 20));
+  if (vec) hipLaunchKernelGGL((gelu_vec<T, TANH>), dim3(grid), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gelu_scalar<T, TANH>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_softmax(NormType t, const RowDesc& d, hipStream_t s) {
+  switch (t) {
+    case NormType::BF16: return run_softmax<NormType::BF16>(d, s);
+    case NormType::F16:  return run_softmax<NormType::F16>(d, s);
+    case NormType::F32:  return run_softmax<NormType::F32>(d, s);
+  }
+  return hipErrorNotSupported;
+}
+
+hipError_t launch_gelu(NormType t, bool tanh_form, const RowDesc& d, hipStream_t s) {
+  switch (t) {
+    case NormType::BF16: return tanh_form ? run_gelu<NormType::BF16, true>(d, s) : run_gelu<NormType::BF16, false>(d, s);
+    case NormType::F16:  return tanh_form ? run_gelu<NormType::F16, true>(d, s) : run_gelu<NormType::F16, false>(d, s);
+    case NormType::F32:  return tanh_form ? run_gelu<NormType::F32, true>(d, s) : run_gelu<NormType::F32, false>(d, s);
+  }
+  return hipErrorNotSupported;
+}
+
+}  // namespace grxk

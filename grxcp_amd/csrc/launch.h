@@ -73,6 +73,17 @@ struct NormDesc {
 hipError_t launch_rmsnorm(NormType t, const NormDesc& d, hipStream_t s);
 hipError_t launch_layernorm(NormType t, const NormDesc& d, hipStream_t s);
 
+// Row-wise softmax over the last dimension and element-wise GELU.
+struct RowDesc {
+  int64_t rows;
+  int hidden;
+  int64_t x_row_stride, y_row_stride;  // elements
+  const void* x;
+  void* y;
+};
+hipError_t launch_softmax(NormType t, const RowDesc& d, hipStream_t s);
+hipError_t launch_gelu(NormType t, bool tanh_form, const RowDesc& d, hipStream_t s);
+
 enum class AttnType { BF16, F16 };
 struct AttnDesc {
   int B, H, S, D;

@@ -90,6 +90,34 @@ grxdnnStatus_t grxdnnLayerNormForward(grxdnnHandle_t handle,
                                       float eps,
                                       grxdnnTensorDescriptor_t yDesc, void* y);
 
+/* ---- softmax (forward) ---------------------------------------------------
+ * Over the last dimension of x, every other dimension a row index:
+ *   y[..., i] = exp(x[..., i] - m) / sum_j exp(x[..., j] - m),  m = max_j x[..., j]
+ * Same layout rules and types as the normalisations above (rows flatten to
+ * one row stride, innermost stride 1; GRX_R_16BF, GRX_R_16F or GRX_R_32F; y
+ * of x's type and shape); fp32 arithmetic, y rounded once. A row whose every
+ * element is -inf gives NaN, as the formula does. hidden: 1 .. 2^24.
+ * (New: planned by ref docs/designs/grxcp_roadmap.md:864-877.) */
+grxdnnStatus_t grxdnnSoftmaxForward(grxdnnHandle_t handle,
+                                    grxdnnTensorDescriptor_t xDesc, const void* x,
+                                    grxdnnTensorDescriptor_t yDesc, void* y);
+
+/* ---- GELU (forward, element-wise) -----------------------------------------
+ *   GRXDNN_GELU_ERF:  y = x/2 * (1 + erf(x / sqrt(2)))
+ *   GRXDNN_GELU_TANH: y = x/2 * (1 + tanh(sqrt(2/pi) * (x + 0.044715 x^3)))
+ * x and y: descriptors of the same shape and type (GRX_R_16BF, GRX_R_16F,
+ * GRX_R_32F) under the row layout rules above; fp32 arithmetic, y rounded
+ * once; y may be x (in place). hidden: 1 .. 2^24.
+ * (New: planned by ref docs/designs/grxcp_roadmap.md:864-877.) */
+typedef enum {
+  GRXDNN_GELU_ERF  = 0,
+  GRXDNN_GELU_TANH = 1
+} grxdnnGeluMode_t;
+
+grxdnnStatus_t grxdnnGeluForward(grxdnnHandle_t handle, grxdnnGeluMode_t mode,
+                                 grxdnnTensorDescriptor_t xDesc, const void* x,
+                                 grxdnnTensorDescriptor_t yDesc, void* y);
+
 /* ---- fused scaled-dot-product attention (forward) ----------------------
  *
  *   O[b,h,i,:] = sum_j softmax_j( scale * <Q[b,h,i,:], K[b,h,j,:]> + mask ) V[b,h,j,:]

@@ -28,6 +28,13 @@ rmsnorm / layernorm    closed forms (constant rows, scale/shift invariance),
 attention_head         closed forms (row 0 -> V[0], Q = 0 -> prefix mean,
                        uniform V), torch scaled_dot_product_attention fp64
                        on CPU, mutation checks
+softmax                closed forms (constant rows -> 1/n, two-element
+                       logistic, shift invariance, rows sum to 1),
+                       torch.softmax fp64 on CPU, mutation check
+gelu                   published values (Phi(1), Phi(2) from the normal
+                       table), the identity gelu(x) - gelu(-x) = x,
+                       torch.nn.functional.gelu fp64 on CPU (both forms),
+                       mutation check
 =====================  =====================================================
 """
 from __future__ import annotations
@@ -85,6 +92,8 @@ def lib():
                                        _f32p, ctypes.c_double, _f32p]
         L.oracle_attention_head.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double,
                                             _f32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int]
+        L.oracle_softmax.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p]
+        L.oracle_gelu.argtypes = [ctypes.c_long, ctypes.c_int, _f32p, _f32p]
         _lib = L
     return _lib
 
@@ -217,6 +226,23 @@ def layernorm(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float) ->
     y = np.empty_like(x)
     lib().oracle_layernorm(rows, hidden, hidden, _p(x, _f32p), _p(g, _f32p), _p(b, _f32p), eps,
                            _p(y, _f32p))
+    return y
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    """Softmax over the last axis of a 2-d float32 array."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, hidden = x.shape
+    y = np.empty_like(x)
+    lib().oracle_softmax(rows, hidden, hidden, _p(x, _f32p), _p(y, _f32p))
+    return y
+
+
+def gelu(x: np.ndarray, mode: int) -> np.ndarray:
+    """GELU element-wise; mode 0 = erf form, 1 = tanh form."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().oracle_gelu(x.size, int(mode), _p(x, _f32p), _p(y, _f32p))
     return y
 
 

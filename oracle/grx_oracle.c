@@ -288,3 +288,34 @@ void oracle_attention_head(int S, int D, int causal, double scale,
     free(p);
   }
 }
+
+/* ---- softmax and GELU -------------------------------------------------- */
+
+void oracle_softmax(int rows, int hidden, int ld, const float* x, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; ++r) {
+    const float* xr = x + (size_t)r * (size_t)ld;
+    float* yr = y + (size_t)r * (size_t)ld;
+    double mx = -INFINITY;
+    for (int c = 0; c < hidden; ++c)
+      if ((double)xr[c] > mx) mx = (double)xr[c];
+    /* mutation 7: the last element is left out of the normaliser */
+    const int terms = (g_mutation == 7 && hidden > 1) ? hidden - 1 : hidden;
+    double sum = 0.0;
+    for (int c = 0; c < terms; ++c) sum += exp((double)xr[c] - mx);
+    for (int c = 0; c < hidden; ++c) yr[c] = (float)(exp((double)xr[c] - mx) / sum);
+  }
+}
+
+void oracle_gelu(long n, int mode, const float* x, float* y) {
+  /* mutation 8: erf(x) in place of erf(x / sqrt 2) */
+  const double k = (g_mutation == 8) ? 1.0 : 1.0 / sqrt(2.0);
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) {
+    const double v = (double)x[i];
+    double g;
+    if (mode == 1) g = 0.5 * v * (1.0 + tanh(sqrt(2.0 / 3.14159265358979323846) * (v + 0.044715 * v * v * v)));
+    else g = 0.5 * v * (1.0 + erf(v * k));
+    y[i] = (float)g;
+  }
+}

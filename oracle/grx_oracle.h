@@ -95,6 +95,14 @@ void oracle_attention_head(int S, int D, int causal, double scale,
                            const float* q, const float* k, const float* v,
                            float* o, int row0, int row1);
 
+/* Softmax over the last dimension of rows with pitch `ld`, fp64 internally:
+ * y = exp(x - max) / sum(exp(x - max)). GELU element-wise, fp64:
+ * mode 0 x/2 (1 + erf(x / sqrt 2)), mode 1 x/2 (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))).
+ * No reference counterpart (grxDNN is unimplemented; planned by
+ * ref docs/designs/grxcp_roadmap.md:864-877). */
+void oracle_softmax(int rows, int hidden, int ld, const float* x, float* y);
+void oracle_gelu(long n, int mode, const float* x, float* y);
+
 #ifdef __cplusplus
 }
 #endif

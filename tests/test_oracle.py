@@ -285,6 +285,39 @@ def test_attention_closed_forms():
     np.testing.assert_allclose(last, O.attention_head(q, k, v, False, 0.3), rtol=1e-5, atol=1e-6)
 
 
+def test_softmax_closed_forms_and_torch():
+    g = np.random.default_rng(11)
+    # constant rows -> 1/n (exact for n a power of two)
+    for n in (1, 8, 1024):
+        y = O.softmax(np.full((3, n), 2.5, np.float32))
+        assert np.array_equal(y, np.full((3, n), 1.0 / n, np.float32))
+    # two elements: the logistic function
+    a, b = 0.75, -1.25
+    y = O.softmax(np.array([[a, b]], np.float32))
+    np.testing.assert_allclose(y[0, 0], 1.0 / (1.0 + np.exp(b - a)), rtol=1e-7)
+    x = (3.0 * g.standard_normal((37, 301))).astype(np.float32)
+    y = O.softmax(x)
+    np.testing.assert_allclose(y.sum(axis=1), 1.0, rtol=1e-6)
+    np.testing.assert_allclose(O.softmax(x + np.float32(7.0)), y, rtol=1e-5, atol=1e-9)
+    ref = torch.softmax(torch.from_numpy(x).double(), dim=1).float().numpy()
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-12)
+
+
+def test_gelu_published_values_identity_and_torch():
+    # Phi(1) = 0.841344746068543, Phi(2) = 0.977249868051821 (standard normal table)
+    x = np.array([0.0, 1.0, -1.0, 2.0], np.float32)
+    y = O.gelu(x, 0)
+    np.testing.assert_allclose(y, [0.0, 0.841344746068543, -0.158655253931457, 2 * 0.977249868051821],
+                               rtol=1e-6, atol=1e-12)
+    g = np.random.default_rng(12)
+    x = (2.5 * g.standard_normal(4001)).astype(np.float32)
+    for mode, approx in ((0, "none"), (1, "tanh")):
+        y, ym = O.gelu(x, mode), O.gelu(-x, mode)
+        np.testing.assert_allclose(y - ym, x, rtol=1e-5, atol=1e-6)   # gelu(x) - gelu(-x) = x
+        ref = torch.nn.functional.gelu(torch.from_numpy(x).double(), approximate=approx).float().numpy()
+        np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-7)
+
+
 # ---- the checks above fail when a mistake is planted --------------------------
 
 @pytest.mark.parametrize("mutation,check", [
@@ -299,6 +332,8 @@ def test_attention_closed_forms():
     (4, lambda: test_attention_vs_torch_sdpa(True)),
     (5, lambda: test_attention_closed_forms()),
     (6, lambda: test_dequant_vs_numpy_and_torch()),
+    (7, lambda: test_softmax_closed_forms_and_torch()),
+    (8, lambda: test_gelu_published_values_identity_and_torch()),
 ])
 def test_planted_mistake_is_caught(mutation, check):
     O.set_mutation(mutation)
