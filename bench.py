@@ -274,6 +274,33 @@ def bench_norm(stream, dnn, layer, steps, warmup, cpu):
     return out
 
 
+def bench_rowop(stream, dnn, op, steps, warmup):
+    """grxdnnSoftmaxForward / grxdnnGeluForward(tanh) on [16384, 8192] bf16."""
+    rows, hidden = 16384, 8192
+    log(f"{op}: generating inputs")
+    xs = [synth.normal_bf16(rows * hidden, 45 + i) for i in range(2)]
+    dx = [g.DeviceBuffer.from_array(x) for x in xs]
+    dy = [g.DeviceBuffer(rows * hidden * 2) for _ in range(2)]
+    xd = g.TensorDesc(BF16, [rows, hidden])
+    state = {"i": 0}
+
+    def launch():
+        i = state["i"] & 1
+        state["i"] += 1
+        s = (dnn.softmax(xd, dx[i].p, xd, dy[i].p) if op == "softmax"
+             else dnn.gelu(g.GELU_TANH, xd, dx[i].p, xd, dy[i].p))
+        if s:
+            raise g.GrxError(f"{op} status {s}")
+    log(f"{op}: timing")
+    ms = time_launches(stream, launch, steps, warmup)
+    moved = rows * hidden * 2 * 2
+    out = {"name": f"{op}_16384x8192", "ms": round(ms, 5), "value": round(moved / ms / 1e6, 1),
+           "unit": "GB/s", "roofline": roofline("hbm", moved, ms, "hbm", op)}
+    for d in dx + dy:
+        d.close()
+    return out
+
+
 def bench_attention(stream, dnn, steps, warmup, cpu):
     B, H, S, D = 4, 32, 4096, 128
     n = B * H * S * D
@@ -311,7 +338,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention,sgemm")
+    ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention,sgemm,softmax,gelu")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy kernel of MIB MiB (torch), "
                          "the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -358,6 +385,10 @@ def main() -> int:
         ops.append(bench_attention(stream, dnn, args.steps, args.warmup, cpu))
     if want("sgemm"):
         ops.append(bench_sgemm(stream, blas, args.steps, args.warmup))
+    if want("softmax"):
+        ops.append(bench_rowop(stream, dnn, "softmax", args.steps, args.warmup))
+    if want("gelu"):
+        ops.append(bench_rowop(stream, dnn, "gelu", args.steps, args.warmup))
 
     if headline is None:
         headline = ops.pop(0)

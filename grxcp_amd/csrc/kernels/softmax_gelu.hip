@@ -7,7 +7,7 @@
 // Softmax, rows of up to 1024 16-byte chunks: one row per wavefront, held
 // packed in registers; the row max and the sum of exp(x - max) are shuffle
 // reductions (no LDS, no barrier); y = exp(x - max) / sum in fp32, rounded
-// once. Longer or unaligned rows: one row per workgroup, three element-wise
+// once (16-bit outputs use the hardware exp2, fp32 the library expf). Longer or unaligned rows: one row per workgroup, three element-wise
 // passes (max, sum, write) re-reading x.
 // GELU: grid-stride over 16-byte chunks of every row (element-wise for
 // unaligned layouts), erf or tanh form in fp32, rounded once.
@@ -18,6 +18,13 @@
 
 namespace grxk {
 namespace {
+
+// exp(d) for d <= 0. 16-bit outputs take the hardware exp2 of d*log2(e)
+// (relative error well under their half ulp); fp32 keeps the library expf.
+template <NormType T> __device__ __forceinline__ float exp_le0(float d) {
+  if constexpr (T == NormType::F32) return expf(d);
+  else return __builtin_amdgcn_exp2f(d * 1.4426950408889634f);
+}
 
 struct RParams {
   const uint8_t* x;
@@ -60,7 +67,7 @@ __global__ __launch_bounds__(256) void softmax_wave(RParams p) {
       float v[V];
       IO::unpack(raw[q], v);
 #pragma unroll
-      for (int e = 0; e < V; ++e) sum += expf(v[e] - mx);
+      for (int e = 0; e < V; ++e) sum += exp_le0<T>(v[e] - mx);
     }
     // Keep only the packed row live between passes.
 #pragma unroll
@@ -73,7 +80,7 @@ __global__ __launch_bounds__(256) void softmax_wave(RParams p) {
       float v[V], o[V];
       IO::unpack(raw[q], v);
 #pragma unroll
-      for (int e = 0; e < V; ++e) o[e] = expf(v[e] - mx) * inv;
+      for (int e = 0; e < V; ++e) o[e] = exp_le0<T>(v[e] - mx) * inv;
       __builtin_nontemporal_store(IO::pack(o), (u32x4*)yrow + c);
     }
   }
@@ -100,16 +107,18 @@ __global__ __launch_bounds__(256) void softmax_rows(RParams p) {
     for (int c = tid; c < p.hidden; c += 256) mx = fmaxf(mx, IO::ld(p.x, xo + c));
     mx = block_reduce(mx, red, true);
     float sum = 0.0f;
-    for (int c = tid; c < p.hidden; c += 256) sum += expf(IO::ld(p.x, xo + c) - mx);
+    for (int c = tid; c < p.hidden; c += 256) sum += exp_le0<T>(IO::ld(p.x, xo + c) - mx);
     const float inv = 1.0f / block_reduce(sum, red, false);
-    for (int c = tid; c < p.hidden; c += 256) IO::st(p.y, yo + c, expf(IO::ld(p.x, xo + c) - mx) * inv);
+    for (int c = tid; c < p.hidden; c += 256) IO::st(p.y, yo + c, exp_le0<T>(IO::ld(p.x, xo + c) - mx) * inv);
   }
 }
 
+// The tanh form uses x/2 (1 + tanh z) = x * sigmoid(2z) = x / (1 + exp(-2z)):
+// one hardware exp2 and one reciprocal instead of a library tanh.
 template <bool TANH> __device__ __forceinline__ float gelu(float x) {
   if (TANH) {
-    const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-    return 0.5f * x * (1.0f + tanhf(k0 * (x + 0.044715f * x * x * x)));
+    const float z = 0.7978845608028654f * (x + 0.044715f * x * x * x);  // sqrt(2/pi)(x + 0.044715 x^3)
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * z));  // 2 log2(e)
   }
   return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
 }
