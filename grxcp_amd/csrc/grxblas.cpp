@@ -163,6 +163,9 @@ grxblasStatus_t probe_for(grxblasContext& ctx, int64_t needed, grxCycleSlot** ou
 
 }  // namespace
 
+// The C API is the only thing these libraries export (built with
+// -fvisibility=hidden).
+#pragma GCC visibility push(default)
 extern "C" {
 
 const char* grxblasGetStatusString(grxblasStatus_t s) {
@@ -472,3 +475,4 @@ grxblasStatus_t grxblasSgemmStridedBatched(grxblasHandle_t handle, grxblasOperat
 }
 
 }  // extern "C"
+#pragma GCC visibility pop

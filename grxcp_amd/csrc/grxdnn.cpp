@@ -203,6 +203,9 @@ grxdnnStatus_t row_common(grxdnnHandle_t handle, grxdnnTensorDescriptor_t xDesc,
 
 }  // namespace
 
+// The C API is the only thing these libraries export (built with
+// -fvisibility=hidden).
+#pragma GCC visibility push(default)
 extern "C" {
 
 const char* grxdnnGetStatusString(grxdnnStatus_t s) {
@@ -412,3 +415,4 @@ grxdnnStatus_t grxdnnAttentionForward(grxdnnHandle_t handle, grxdnnAttentionDesc
 }
 
 }  // extern "C"
+#pragma GCC visibility pop

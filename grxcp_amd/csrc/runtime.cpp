@@ -44,33 +44,9 @@ hipEvent_t he(grxEvent_t e) { return reinterpret_cast<hipEvent_t>(e); }
 
 }  // namespace
 
-// One table from HIP's error space to grx's (the role of the reference's
-// error map, ref src/runtime/error.cpp:9-24).
-grxError_t grx_from_hip(hipError_t e) {
-  switch (e) {
-    case hipSuccess:                    return grxSuccess;
-    case hipErrorInvalidValue:          return grxErrorInvalidValue;
-    case hipErrorOutOfMemory:           return grxErrorMemoryAllocation;
-    case hipErrorNotInitialized:        return grxErrorInitializationError;
-    case hipErrorNoDevice:
-    case hipErrorInvalidDevice:         return grxErrorInvalidDevice;
-    case hipErrorInvalidDevicePointer:  return grxErrorInvalidDevicePointer;
-    case hipErrorInvalidMemcpyDirection:return grxErrorInvalidMemcpyDirection;
-    case hipErrorInvalidHandle:         return grxErrorInvalidResourceHandle;
-    case hipErrorNotReady:              return grxErrorNotReady;
-    case hipErrorNotSupported:          return grxErrorNotSupported;
-    case hipErrorInvalidImage:
-    case hipErrorNoBinaryForGpu:        return grxErrorInvalidKernelImage;
-    case hipErrorInvalidDeviceFunction: return grxErrorInvalidDeviceFunction;
-    case hipErrorLaunchFailure:         return grxErrorLaunchFailure;
-    case hipErrorLaunchOutOfResources:  return grxErrorLaunchOutOfResources;
-    case hipErrorLaunchTimeOut:         return grxErrorTimeout;
-    case hipErrorFileNotFound:          return grxErrorFileNotFound;
-    case hipErrorInvalidSymbol:         return grxErrorInvalidSymbol;
-    default:                            return grxErrorUnknown;
-  }
-}
-
+// The C API is the only thing these libraries export (built with
+// -fvisibility=hidden).
+#pragma GCC visibility push(default)
 extern "C" {
 
 const char* grxGetErrorName(grxError_t e) {
@@ -344,3 +320,4 @@ grxError_t grxEventElapsedTime(float* ms, grxEvent_t start, grxEvent_t end) {
 }
 
 }  // extern "C"
+#pragma GCC visibility pop

@@ -51,6 +51,12 @@ def test_every_declared_symbol_is_exported(header):
     assert not missing, f"{HEADERS[header]} lacks {missing}"
 
 
+@pytest.mark.parametrize("header", sorted(HEADERS))
+def test_nothing_but_the_declared_api_is_exported(header):
+    extra = sorted(exported(HEADERS[header]) - set(declared(header)))
+    assert not extra, f"{HEADERS[header]} also exports {extra[:10]}"
+
+
 def test_python_table_matches_headers():
     for header, lib in HEADERS.items():
         assert set(declared(header)) == set(g.EXPORTS[lib]), header
