@@ -33,9 +33,12 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float((uint32_t)b << 16);
 }
 
-// Two fp32 -> packed bf16x2 (low half = a), RNE.
+// Two fp32 -> packed bf16x2 (low half = a) in one v_cvt_pk_bf16_f32: round
+// to nearest even, NaN quieted -- the same bits as f32_to_bf16 on each half.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // fp32 <-> fp16 through the hardware converts (v_cvt_f16_f32 rounds to
@@ -47,6 +50,13 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
 
 __device__ __forceinline__ float f16_to_f32(uint16_t b) {
   return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// Two fp32 -> packed fp16x2 (low half = a), round to nearest even.
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  const f16x2 v = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // ---- reductions over one 64-wide wavefront ---------------------------------

@@ -82,7 +82,9 @@ struct KParams {
 };
 
 // ---------------------------------------------------------------------------
-// epilogue: 4 consecutive rows i0..i0+3 of column j
+// epilogue. C is column-major, so a run of consecutive rows i0.. of one column
+// j is contiguous. Each Epi writes one element (put) or a full aligned run of
+// kRun elements, 16 bytes, with one vector access (put_run).
 // ---------------------------------------------------------------------------
 
 template <MmaOut OUT>
@@ -90,30 +92,35 @@ struct Epi;
 
 template <>
 struct Epi<MmaOut::F32> {
+  using T = float;
+  static constexpr int kRun = 4;
   __device__ static float apply(const KParams& p, float acc, float c_old) {
     // alpha*acc (+ beta*C) with each operation rounded separately, as the
     // reference's CPU gate writes it (no contraction into an FMA).
     const float s = __fmul_rn(p.alpha, acc);
     return p.beta == 0.0f ? s : __fadd_rn(s, __fmul_rn(p.beta, c_old));
   }
-  __device__ static void store4(const KParams& p, int i0, int j, const float v[4], bool vec) {
-    float* c = (float*)p.c + (int64_t)j * p.ldc + i0;
-    if (vec) {
-      f32x4 old = {0, 0, 0, 0};
-      if (p.beta != 0.0f) old = *(const f32x4*)c;
-      f32x4 o;
-      o.x = apply(p, v[0], old.x); o.y = apply(p, v[1], old.y);
-      o.z = apply(p, v[2], old.z); o.w = apply(p, v[3], old.w);
-      *(f32x4*)c = o;
+  __device__ static void put(const KParams& p, T* c, float v, int) {
+    *c = apply(p, v, p.beta != 0.0f ? *c : 0.0f);
+  }
+  __device__ static void put_run(const KParams& p, T* c, const float* v, int) {
+    f32x4 o;
+    if (p.beta == 0.0f) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = __fmul_rn(p.alpha, v[q]);
     } else {
-      for (int q = 0; q < 4; ++q)
-        if (i0 + q < p.m) c[q] = apply(p, v[q], p.beta != 0.0f ? c[q] : 0.0f);
+      const f32x4 old = *(const f32x4*)c;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = apply(p, v[q], old[q]);
     }
+    *(f32x4*)c = o;
   }
 };
 
 template <MmaOut OUT>
 struct EpiNarrow {
+  using T = uint16_t;
+  static constexpr int kRun = 8;
   __device__ static uint16_t cvt(float x) {
     if constexpr (OUT == MmaOut::BF16) return f32_to_bf16(x);
     else return f32_to_f16(x);
@@ -126,21 +133,27 @@ struct EpiNarrow {
     const float s = __fmul_rn(p.alpha, acc);
     return p.beta == 0.0f ? s : __fadd_rn(s, __fmul_rn(p.beta, back(c_old)));
   }
-  __device__ static void store4(const KParams& p, int i0, int j, const float v[4], bool vec) {
-    uint16_t* c = (uint16_t*)p.c + (int64_t)j * p.ldc + i0;
-    if (vec) {
-      u32x2 old = {0, 0};
-      if (p.beta != 0.0f) old = *(const u32x2*)c;
-      u32x2 o;
-      o.x = (uint32_t)cvt(apply(p, v[0], (uint16_t)(old.x & 0xffff))) |
-            ((uint32_t)cvt(apply(p, v[1], (uint16_t)(old.x >> 16))) << 16);
-      o.y = (uint32_t)cvt(apply(p, v[2], (uint16_t)(old.y & 0xffff))) |
-            ((uint32_t)cvt(apply(p, v[3], (uint16_t)(old.y >> 16))) << 16);
-      *(u32x2*)c = o;
+  __device__ static void put(const KParams& p, T* c, float v, int) {
+    *c = cvt(apply(p, v, p.beta != 0.0f ? *c : (uint16_t)0));
+  }
+  __device__ static uint32_t pack(float a, float b) {
+    if constexpr (OUT == MmaOut::BF16) return pack_bf16x2(a, b);
+    else return pack_f16x2(a, b);
+  }
+  __device__ static void put_run(const KParams& p, T* c, const float* v, int) {
+    u32x4 o;
+    if (p.beta == 0.0f) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        o[h] = pack(__fmul_rn(p.alpha, v[2 * h]), __fmul_rn(p.alpha, v[2 * h + 1]));
     } else {
-      for (int q = 0; q < 4; ++q)
-        if (i0 + q < p.m) c[q] = cvt(apply(p, v[q], p.beta != 0.0f ? c[q] : (uint16_t)0));
+      const u32x4 old = *(const u32x4*)c;
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        o[h] = pack(apply(p, v[2 * h], (uint16_t)(old[h] & 0xffff)),
+                    apply(p, v[2 * h + 1], (uint16_t)(old[h] >> 16)));
     }
+    *(u32x4*)c = o;
   }
 };
 template <> struct Epi<MmaOut::BF16> : EpiNarrow<MmaOut::BF16> {};
@@ -148,53 +161,66 @@ template <> struct Epi<MmaOut::F16> : EpiNarrow<MmaOut::F16> {};
 
 template <>
 struct Epi<MmaOut::I32> {
+  using T = int;
+  static constexpr int kRun = 4;
   __device__ static int apply(const KParams& p, int acc, int c_old) {
     uint32_t r = (uint32_t)p.ialpha * (uint32_t)acc;
     if (p.ibeta != 0) r += (uint32_t)p.ibeta * (uint32_t)c_old;
     return (int)r;
   }
-  __device__ static void store4(const KParams& p, int i0, int j, const int v[4], bool vec) {
-    int* c = (int*)p.c + (int64_t)j * p.ldc + i0;
-    if (vec) {
-      i32x4 old = {0, 0, 0, 0};
-      if (p.ibeta != 0) old = *(const i32x4*)c;
-      i32x4 o;
-      o.x = apply(p, v[0], old.x); o.y = apply(p, v[1], old.y);
-      o.z = apply(p, v[2], old.z); o.w = apply(p, v[3], old.w);
-      *(i32x4*)c = o;
-    } else {
-      for (int q = 0; q < 4; ++q)
-        if (i0 + q < p.m) c[q] = apply(p, v[q], p.ibeta != 0 ? c[q] : 0);
-    }
+  __device__ static void put(const KParams& p, T* c, int v, int) {
+    *c = apply(p, v, p.ibeta != 0 ? *c : 0);
+  }
+  __device__ static void put_run(const KParams& p, T* c, const int* v, int) {
+    i32x4 old = {0, 0, 0, 0};
+    if (p.ibeta != 0) old = *(const i32x4*)c;
+    i32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = apply(p, v[q], old[q]);
+    *(i32x4*)c = o;
   }
 };
 
 template <>
 struct Epi<MmaOut::DEQ_BF16> {
+  using T = uint16_t;
+  static constexpr int kRun = 8;
   // bf16_rne(f32_rne(f32_rne(acc) * scale[j])): v_cvt_f32_i32 rounds to
   // nearest even, __fmul_rn is one correctly rounded product.
   __device__ static uint16_t apply(float s, int acc) {
     return f32_to_bf16(__fmul_rn((float)acc, s));
   }
-  __device__ static void store4(const KParams& p, int i0, int j, const int v[4], bool vec) {
-    uint16_t* c = (uint16_t*)p.c + (int64_t)j * p.ldc + i0;
+  __device__ static void put(const KParams& p, T* c, int v, int j) { *c = apply(p.scale[j], v); }
+  __device__ static void put_run(const KParams& p, T* c, const int* v, int j) {
     const float s = p.scale[j];
-    if (vec) {
-      u32x2 o;
-      o.x = (uint32_t)apply(s, v[0]) | ((uint32_t)apply(s, v[1]) << 16);
-      o.y = (uint32_t)apply(s, v[2]) | ((uint32_t)apply(s, v[3]) << 16);
-      *(u32x2*)c = o;
-    } else {
-      for (int q = 0; q < 4; ++q)
-        if (i0 + q < p.m) c[q] = apply(s, v[q]);
-    }
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      o[h] = pack_bf16x2(__fmul_rn((float)v[2 * h], s), __fmul_rn((float)v[2 * h + 1], s));
+    *(u32x4*)c = o;
   }
 };
 
-// Spread a 32x32 accumulator tile (rows base_i.., cols base_j..) to C.
+// `count` consecutive rows i0.. of column j (j < n). With `vec`, the caller
+// guarantees a run of kRun elements starting at i0 is 16-byte aligned.
+template <MmaOut OUT, class E>
+__device__ __forceinline__ void store_run(const KParams& p, int i0, int j, const E* v, int count,
+                                          bool vec) {
+  using P = Epi<OUT>;
+  typename P::T* c = (typename P::T*)p.c + (int64_t)j * p.ldc + i0;
+  if (vec && count == P::kRun && i0 + P::kRun <= p.m) {
+    P::put_run(p, c, v, j);
+  } else {
+    for (int q = 0; q < count; ++q)
+      if (i0 + q < p.m) P::put(p, c + q, v[q], j);
+  }
+}
+
+// Spread a 32x32 accumulator tile (rows base_i.., cols base_j..) to C, four
+// rows per lane and store (general path: no alignment assumed).
 template <class Op, MmaOut OUT>
 __device__ __forceinline__ void store_acc_tile(const KParams& p, const typename Op::Acc& acc,
-                                               int base_i, int base_j, int lane, bool vec_ok) {
+                                               int base_i, int base_j, int lane) {
   using E = typename Op::Elem;
   const int j = base_j + (lane & 31);
   if (j >= p.n) return;
@@ -203,9 +229,20 @@ __device__ __forceinline__ void store_acc_tile(const KParams& p, const typename 
     const int i0 = base_i + 8 * g + 4 * (lane >> 5);
     if (i0 >= p.m) continue;
     E v[4] = {(E)acc[4 * g + 0], (E)acc[4 * g + 1], (E)acc[4 * g + 2], (E)acc[4 * g + 3]};
-    Epi<OUT>::store4(p, i0, j, v, vec_ok && (i0 + 3 < p.m));
+    store_run<OUT>(p, i0, j, v, 4, false);
   }
 }
+
+// 32-bit reinterpretation through a by-value copy. (hipcc lowers
+// __builtin_bit_cast applied directly to an element of an ext_vector_type
+// as a cast of element 0, so vector elements always pass through these.)
+template <int N>
+struct IntC { static constexpr int value = N; };
+
+template <class T>
+__device__ __forceinline__ int bits_of(T x) { return __builtin_bit_cast(int, x); }
+template <class T>
+__device__ __forceinline__ T from_bits(int x) { return __builtin_bit_cast(T, x); }
 
 // XCD-aware tile order. Consecutive workgroup ids are dispatched round-robin
 // over the 8 XCDs; remapping gives each XCD a contiguous run of logical tiles,
@@ -364,14 +401,62 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
     phase(1, cur ^ 1, 0, kt + 2, cur, 0);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // no LDS write may outlive the loop
+  __syncthreads();                                     // and no wave still reads a stage
 
-  const bool vec_ok = true;  // host guarantees ldc % 8 == 0 and an aligned C
+  // Epilogue through LDS. A lane's accumulators are 4-row pieces of 32
+  // different columns; stored as they are, every vector store would touch 32
+  // cache lines 16 bytes at a time. Instead each wave parks one 128x32 column
+  // block of raw 32-bit accumulators in its own LDS region ([col][row], pitch
+  // 132 words) and reads it back as runs of kRun rows of one column, so one
+  // store instruction writes whole 256-byte (or 512-byte) column segments.
+  // Rows 64..127 sit 4 words further on (row r at r + 4*(r/64 & 1)): that
+  // keeps the 16 lanes of one column on distinct banks when they read their
+  // runs, with every offset on the write side a compile-time constant.
+  using E = typename Op::Elem;
+  constexpr int kRun = Epi<OUT>::kRun;            // 8 (16-bit C) or 4 (32-bit C)
+  constexpr int kPitch = 128 + 4;
+  constexpr int kLanesPerCol = 128 / kRun;        // 16 or 32
+  constexpr int kColsPerRound = 64 / kLanesPerCol;
+  int* stage = (int*)&lds[0][0][0] + wave * 32 * kPitch;   // 16.5 KB per wave
+  const int run = lane % kLanesPerCol;
+  const int rcol = lane / kLanesPerCol;
+  const int run_pos = run * kRun + 4 * ((run * kRun >> 6) & 1);
+  const int gi = row0 + wm * 128 + run * kRun;
+  // One column block per call; J is a compile-time constant so that acc stays
+  // in registers (a run-time index would move the accumulators to scratch).
+  auto column_block = [&](auto jc) __attribute__((always_inline)) {
+    constexpr int j = decltype(jc)::value;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      store_acc_tile<Op, OUT>(p, acc[i][j], row0 + wm * 128 + i * 32, col0 + wn * 128 + j * 32,
-                              lane, vec_ok);
+      for (int g = 0; g < 4; ++g) {
+        i32x4 w;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w[q] = bits_of(acc[i][j][4 * g + q]);
+        *(i32x4*)&stage[r32 * kPitch + 32 * i + 8 * g + 4 * hh + 4 * (i >> 1)] = w;
+      }
+    // LDS operations of one wave complete in order; the compiler only must
+    // not move the reads above the writes (or the next writes above them).
+    asm volatile("" ::: "memory");
+    for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
+      const int col = rd * kColsPerRound + rcol;
+      const int* src = &stage[col * kPitch + run_pos];
+      E v[kRun];
+#pragma unroll
+      for (int h = 0; h < kRun / 4; ++h) {
+        const i32x4 w = *(const i32x4*)(src + 4 * h);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[4 * h + q] = from_bits<E>(w[q]);
+      }
+      const int gj = col0 + wn * 128 + 32 * j + col;
+      if (gj < p.n && gi < p.m) store_run<OUT>(p, gi, gj, v, kRun, true);
+    }
+    asm volatile("" ::: "memory");
+  };
+  column_block(IntC<0>{});
+  column_block(IntC<1>{});
+  column_block(IntC<2>{});
+  column_block(IntC<3>{});
 
   cycle_record(p.probe, t0, blockIdx.x * 4 + wave, wave);
 }
@@ -457,7 +542,7 @@ __global__ __launch_bounds__(256) void gemm_general(KParams p) {
     __syncthreads();
   }
 
-  store_acc_tile<Op, OUT>(p, acc, row0 + wm * 32, col0 + wn * 32, lane, false);
+  store_acc_tile<Op, OUT>(p, acc, row0 + wm * 32, col0 + wn * 32, lane);
   cycle_record(p.probe, t0, blockIdx.x * 4 + wave, wave);
 }
 
@@ -480,17 +565,17 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   p.probe = d.probe;
 
   constexpr int EB = Op::kElemBytes;
-  const int out_bytes = (OUT == MmaOut::F32 || OUT == MmaOut::I32) ? 4 : 2;
   // The fast path needs K-contiguous operands whose rows start on 16-byte
   // boundaries (so every staged chunk is one aligned 16-byte load), 32-bit
-  // buffer offsets within a 256-row panel, and a C whose 4-row groups are
-  // aligned for one vector store.
+  // buffer offsets within a 256-row panel, and a C whose columns start on
+  // 16-byte boundaries (ldc % 8 == 0, aligned C), so that a run of 4 (32-bit)
+  // or 8 (16-bit) rows of one column is one vector store.
   const bool fast =
       d.ta && !d.tb && d.k > 0 &&
       ((int64_t)d.k * EB) % 16 == 0 &&
       (d.lda * EB) % 16 == 0 && (d.ldb * EB) % 16 == 0 &&
       ((uintptr_t)d.a % 16) == 0 && ((uintptr_t)d.b % 16) == 0 &&
-      d.ldc % 8 == 0 && ((uintptr_t)d.c % (4 * out_bytes)) == 0 &&
+      d.ldc % 8 == 0 && ((uintptr_t)d.c % 16) == 0 &&
       (int64_t)kFastTile * d.lda * EB < (1ll << 31) &&
       (int64_t)kFastTile * d.ldb * EB < (1ll << 31);
   if (fast) {
