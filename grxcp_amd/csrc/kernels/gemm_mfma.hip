@@ -345,32 +345,42 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
 
   // Fragment reads: A rows wm*128 + 32t + r32, B rows wn*128 + 32t + r32,
   // 16 bytes at logical chunk 2*ks + hh. Two register sets: the reads for
-  // k-step ks+1 are in flight while the 16 MFMAs of k-step ks run.
+  // k-step ks+1 are in flight while the 16 MFMAs of k-step ks run. Read slot
+  // q follows first use in the next k-step (A0, B0..B3, A1..A3), so each
+  // read has at least five MFMA pairs to land before an MFMA needs it.
   i32x4 fa[2][4], fb[2][4];
-  auto frag = [&](int st, int ks, int buf, int q) {  // q: 0..3 A, 4..7 B
+  auto frag = [&](int st, int ks, int buf, int q) {
     const int kc = 2 * ks + hh;
-    const int t = q & 3;
-    if (q < 4) {
-      const int ar = wm * 128 + t * 32 + r32;
-      fa[buf][t] = lds[st][0][ar * kChunks + (kc ^ swz(ar))];
-    } else {
+    if (q >= 1 && q <= 4) {
+      const int t = q - 1;
       const int br = wn * 128 + t * 32 + r32;
       fb[buf][t] = lds[st][1][br * kChunks + (kc ^ swz(br))];
+    } else {
+      const int t = q == 0 ? 0 : q - 4;
+      const int ar = wm * 128 + t * 32 + r32;
+      fa[buf][t] = lds[st][0][ar * kChunks + (kc ^ swz(ar))];
     }
+  };
+
+  // A stage is 16 DMA instructions, d = 0..15: 8-row block group
+  // 4*(d/8) + d%4 of operand (d/4)%2.
+  auto dma_d = [&](int kt, int st, int d) {
+    dma(kt, st, 4 * (d >> 3) + (d & 3), (d >> 2) & 1);
   };
 
   // One k-step: 16 MFMAs on register set `buf`; behind every pair of MFMAs
   // one fragment read for the next k-step and, in the phases that carry DMA,
-  // one DMA instruction. The explicit order, held by sched_barrier, keeps the
-  // wave from stalling on a burst of DMA issues while its matrix core idles.
-  auto phase = [&](int buf, int rd_st, int rd_ks, int dma_kt, int dma_st, int dma_half) {
+  // DMA instructions d0 .. d0+cnt-1 spread evenly over the 8 slots. The
+  // explicit order, held by sched_barrier, keeps the wave from stalling on a
+  // burst of DMA issues while its matrix core idles.
+  auto phase = [&](int buf, int rd_st, int rd_ks, int dma_kt, int dma_st, int d0, int cnt) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int i = q >> 1, j0 = 2 * (q & 1);
       acc[i][j0] = Op::mma(fa[buf][i], fb[buf][j0], acc[i][j0]);
       acc[i][j0 + 1] = Op::mma(fa[buf][i], fb[buf][j0 + 1], acc[i][j0 + 1]);
       frag(rd_st, rd_ks, buf ^ 1, q);
-      if (dma_half >= 0) dma(dma_kt, dma_st, 4 * dma_half + (q & 3), q >> 2);
+      if ((q + 1) * cnt / 8 > q * cnt / 8) dma_d(dma_kt, dma_st, d0 + q * cnt / 8);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -380,25 +390,26 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
   // stage kt just vacated) is issued half right after that barrier and half
   // during k-step 0 of the next iteration, so each load has two to four
   // k-steps of MFMA time to land before the barrier that publishes it.
+  // (Measured: moving part of it into k-step 1 saves less DMA issue time
+  // than the late loads then cost at the barrier.)
+  constexpr int kDmaD = 8, kDmaA = 8;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) dma(0, 0, q & 3, q >> 2);
+  for (int d = 0; d < 16; ++d) dma_d(0, 0, d);
 #pragma unroll
-  for (int q = 0; q < 8; ++q) dma(0, 0, 4 + (q & 3), q >> 2);
-#pragma unroll
-  for (int q = 0; q < 8; ++q) dma(1, 1, q & 3, q >> 2);
-  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");   // stage 0 landed; stage 1 half 0 may fly
+  for (int d = 0; d < kDmaD; ++d) dma_d(1, 1, d);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaD) : "memory");  // stage 0 landed
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < 8; ++q) frag(0, 0, 0, q);
 
   for (int kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
-    phase(0, cur, 1, kt + 1, cur ^ 1, 1);
-    phase(1, cur, 2, 0, 0, -1);
-    phase(0, cur, 3, 0, 0, -1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 (both halves) landed
+    phase(0, cur, 1, kt + 1, cur ^ 1, kDmaD, kDmaA);
+    phase(1, cur, 2, 0, 0, 0, 0);
+    phase(0, cur, 3, 0, 0, 0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 landed
     __syncthreads();
-    phase(1, cur ^ 1, 0, kt + 2, cur, 0);
+    phase(1, cur ^ 1, 0, kt + 2, cur, 0, kDmaD);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // no LDS write may outlive the loop
   __syncthreads();                                     // and no wave still reads a stage
@@ -438,18 +449,35 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
     // LDS operations of one wave complete in order; the compiler only must
     // not move the reads above the writes (or the next writes above them).
     asm volatile("" ::: "memory");
-    for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
-      const int col = rd * kColsPerRound + rcol;
+    auto read_run = [&](int col, E* v) __attribute__((always_inline)) {
       const int* src = &stage[col * kPitch + run_pos];
-      E v[kRun];
 #pragma unroll
       for (int h = 0; h < kRun / 4; ++h) {
         const i32x4 w = *(const i32x4*)(src + 4 * h);
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[4 * h + q] = from_bits<E>(w[q]);
       }
-      const int gj = col0 + wn * 128 + 32 * j + col;
-      if (gj < p.n && gi < p.m) store_run<OUT>(p, gi, gj, v, kRun, true);
+    };
+    const int gj0 = col0 + wn * 128 + 32 * j;
+    if (row0 + wm * 128 + 128 <= p.m && gj0 + 32 <= p.n) {
+      // Interior block (the common case): unrolled, no masks.
+      using T = typename Epi<OUT>::T;
+      T* cbase = (T*)p.c + (int64_t)gj0 * p.ldc + gi;
+#pragma unroll
+      for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
+        const int col = rd * kColsPerRound + rcol;
+        E v[kRun];
+        read_run(col, v);
+        Epi<OUT>::put_run(p, cbase + (int64_t)col * p.ldc, v, gj0 + col);
+      }
+    } else {
+      for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
+        const int col = rd * kColsPerRound + rcol;
+        E v[kRun];
+        read_run(col, v);
+        const int gj = gj0 + col;
+        if (gj < p.n && gi < p.m) store_run<OUT>(p, gi, gj, v, kRun, true);
+      }
     }
     asm volatile("" ::: "memory");
   };
