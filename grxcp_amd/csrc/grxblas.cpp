@@ -161,6 +161,70 @@ grxblasStatus_t probe_for(grxblasContext& ctx, int64_t needed, grxCycleSlot** ou
   return GRXBLAS_STATUS_SUCCESS;
 }
 
+// GemmEx and its strided batch. Validation order of ref
+// src/libs/grxblas/grxblas.cpp:507-524, the batch count checked where
+// SgemmStridedBatched checks it.
+grxblasStatus_t gemm_ex_batched(grxblasHandle_t handle, grxblasOperation_t transa,
+                                grxblasOperation_t transb, int m, int n, int k,
+                                const float* alpha, const void* A, grxDataType_t Atype, int lda,
+                                long long strideA, const void* B, grxDataType_t Btype, int ldb,
+                                long long strideB, const float* beta, void* C,
+                                grxDataType_t Ctype, int ldc, long long strideC, int batch) {
+  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  if (!alpha || !beta) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m < 0 || n < 0 || k < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (batch < 0) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (m == 0 || n == 0 || batch == 0) return GRXBLAS_STATUS_SUCCESS;
+  if (k > 0 && (!A || !B)) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (!C) return GRXBLAS_STATUS_INVALID_VALUE;
+  const bool ta = (transa == GRXBLAS_OP_T);
+  const bool tb = (transb == GRXBLAS_OP_T);
+  if (lda < (ta ? k : m) || ldb < (tb ? n : k) || ldc < m) return GRXBLAS_STATUS_INVALID_VALUE;
+  if (batch > 65535) return GRXBLAS_STATUS_NOT_SUPPORTED;
+
+  const grxblasStatus_t s = ensure_ready(*handle);
+  if (s != GRXBLAS_STATUS_SUCCESS) return s;
+
+  // Type pairing after the device is known (ref grxblas.cpp:552-575).
+  grxk::MmaIn in;
+  grxk::MmaOut out;
+  if (Atype == GRX_R_16F && Btype == GRX_R_16F && Ctype == GRX_R_32F) {
+    in = grxk::MmaIn::F16; out = grxk::MmaOut::F32;
+  } else if (Atype == GRX_R_16F && Btype == GRX_R_16F && Ctype == GRX_R_16F) {
+    in = grxk::MmaIn::F16; out = grxk::MmaOut::F16;
+  } else if (Atype == GRX_R_16BF && Btype == GRX_R_16BF && Ctype == GRX_R_32F) {
+    in = grxk::MmaIn::BF16; out = grxk::MmaOut::F32;
+  } else if (Atype == GRX_R_16BF && Btype == GRX_R_16BF && Ctype == GRX_R_16BF) {
+    in = grxk::MmaIn::BF16; out = grxk::MmaOut::BF16;
+  } else if (Atype == GRX_R_8I && Btype == GRX_R_8I && Ctype == GRX_R_32I) {
+    in = grxk::MmaIn::I8; out = grxk::MmaOut::I32;
+  } else {
+    say_types_once();
+    return GRXBLAS_STATUS_NOT_SUPPORTED;
+  }
+  // Integral alpha/beta for the int8 pairing (ref grxblas.cpp:577-584).
+  if (in == grxk::MmaIn::I8 && (!integral(*alpha) || !integral(*beta)))
+    return GRXBLAS_STATUS_INVALID_VALUE;
+
+  grxCycleSlot* probe = nullptr;
+  const grxblasStatus_t ps =
+      probe_for(*handle, grxk::gemm_probe_slots(m, n) * (int64_t)batch, &probe);
+  if (ps != GRXBLAS_STATUS_SUCCESS) return ps;
+
+  grxk::GemmDesc d{};
+  d.m = m; d.n = n; d.k = k;
+  d.ta = ta; d.tb = tb;
+  d.a = A; d.lda = lda;
+  d.b = B; d.ldb = ldb;
+  d.c = C; d.ldc = ldc;
+  d.alpha = *alpha; d.beta = *beta;
+  if (in == grxk::MmaIn::I8) { d.ialpha = (int32_t)*alpha; d.ibeta = (int32_t)*beta; }
+  d.probe = probe;
+  d.batch = batch;
+  d.stride_a = strideA; d.stride_b = strideB; d.stride_c = strideC;
+  return from_hip(grxk::launch_mma_gemm(in, out, d, handle->stream));
+}
+
 }  // namespace
 
 // The C API is the only thing these libraries export (built with
@@ -246,55 +310,20 @@ grxblasStatus_t grxblasGemmEx(grxblasHandle_t handle, grxblasOperation_t transa,
                               const float* alpha, const void* A, grxDataType_t Atype, int lda,
                               const void* B, grxDataType_t Btype, int ldb, const float* beta,
                               void* C, grxDataType_t Ctype, int ldc) {
-  // Validation order of ref src/libs/grxblas/grxblas.cpp:507-524.
-  if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
-  if (!alpha || !beta) return GRXBLAS_STATUS_INVALID_VALUE;
-  if (m < 0 || n < 0 || k < 0) return GRXBLAS_STATUS_INVALID_VALUE;
-  if (m == 0 || n == 0) return GRXBLAS_STATUS_SUCCESS;
-  if (k > 0 && (!A || !B)) return GRXBLAS_STATUS_INVALID_VALUE;
-  if (!C) return GRXBLAS_STATUS_INVALID_VALUE;
-  const bool ta = (transa == GRXBLAS_OP_T);
-  const bool tb = (transb == GRXBLAS_OP_T);
-  if (lda < (ta ? k : m) || ldb < (tb ? n : k) || ldc < m) return GRXBLAS_STATUS_INVALID_VALUE;
+  return gemm_ex_batched(handle, transa, transb, m, n, k, alpha, A, Atype, lda, 0, B, Btype,
+                         ldb, 0, beta, C, Ctype, ldc, 0, 1);
+}
 
-  const grxblasStatus_t s = ensure_ready(*handle);
-  if (s != GRXBLAS_STATUS_SUCCESS) return s;
-
-  // Type pairing after the device is known (ref grxblas.cpp:552-575).
-  grxk::MmaIn in;
-  grxk::MmaOut out;
-  if (Atype == GRX_R_16F && Btype == GRX_R_16F && Ctype == GRX_R_32F) {
-    in = grxk::MmaIn::F16; out = grxk::MmaOut::F32;
-  } else if (Atype == GRX_R_16F && Btype == GRX_R_16F && Ctype == GRX_R_16F) {
-    in = grxk::MmaIn::F16; out = grxk::MmaOut::F16;
-  } else if (Atype == GRX_R_16BF && Btype == GRX_R_16BF && Ctype == GRX_R_32F) {
-    in = grxk::MmaIn::BF16; out = grxk::MmaOut::F32;
-  } else if (Atype == GRX_R_16BF && Btype == GRX_R_16BF && Ctype == GRX_R_16BF) {
-    in = grxk::MmaIn::BF16; out = grxk::MmaOut::BF16;
-  } else if (Atype == GRX_R_8I && Btype == GRX_R_8I && Ctype == GRX_R_32I) {
-    in = grxk::MmaIn::I8; out = grxk::MmaOut::I32;
-  } else {
-    say_types_once();
-    return GRXBLAS_STATUS_NOT_SUPPORTED;
-  }
-  // Integral alpha/beta for the int8 pairing (ref grxblas.cpp:577-584).
-  if (in == grxk::MmaIn::I8 && (!integral(*alpha) || !integral(*beta)))
-    return GRXBLAS_STATUS_INVALID_VALUE;
-
-  grxCycleSlot* probe = nullptr;
-  const grxblasStatus_t ps = probe_for(*handle, grxk::gemm_probe_slots(m, n), &probe);
-  if (ps != GRXBLAS_STATUS_SUCCESS) return ps;
-
-  grxk::GemmDesc d{};
-  d.m = m; d.n = n; d.k = k;
-  d.ta = ta; d.tb = tb;
-  d.a = A; d.lda = lda;
-  d.b = B; d.ldb = ldb;
-  d.c = C; d.ldc = ldc;
-  d.alpha = *alpha; d.beta = *beta;
-  if (in == grxk::MmaIn::I8) { d.ialpha = (int32_t)*alpha; d.ibeta = (int32_t)*beta; }
-  d.probe = probe;
-  return from_hip(grxk::launch_mma_gemm(in, out, d, handle->stream));
+grxblasStatus_t grxblasGemmStridedBatchedEx(grxblasHandle_t handle, grxblasOperation_t transa,
+                                            grxblasOperation_t transb, int m, int n, int k,
+                                            const float* alpha, const void* A,
+                                            grxDataType_t Atype, int lda, long long strideA,
+                                            const void* B, grxDataType_t Btype, int ldb,
+                                            long long strideB, const float* beta, void* C,
+                                            grxDataType_t Ctype, int ldc, long long strideC,
+                                            int batchCount) {
+  return gemm_ex_batched(handle, transa, transb, m, n, k, alpha, A, Atype, lda, strideA, B,
+                         Btype, ldb, strideB, beta, C, Ctype, ldc, strideC, batchCount);
 }
 
 grxblasStatus_t grxblasGemmExDequant(grxblasHandle_t handle, grxblasOperation_t transa,

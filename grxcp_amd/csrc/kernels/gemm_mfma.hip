@@ -77,6 +77,7 @@ struct KParams {
   int ta, tb;             // general kernel only
   float alpha, beta;
   int32_t ialpha, ibeta;
+  int64_t sa, sb, sc;     // batch strides in bytes (grid.y is the batch)
   const float* scale;
   grxCycleSlot* probe;
 };
@@ -244,6 +245,21 @@ __device__ __forceinline__ int bits_of(T x) { return __builtin_bit_cast(int, x);
 template <class T>
 __device__ __forceinline__ T from_bits(int x) { return __builtin_bit_cast(T, x); }
 
+// The problem of batch blockIdx.y: operands and C moved by its strides.
+__device__ __forceinline__ KParams batch_view(const KParams& in) {
+  KParams p = in;
+  const int64_t z = blockIdx.y;
+  p.a += z * in.sa;
+  p.b += z * in.sb;
+  p.c = (uint8_t*)in.c + z * in.sc;
+  return p;
+}
+
+// Probe slot of a wave: workgroups of all batches in launch order.
+__device__ __forceinline__ int64_t probe_slot(int wave) {
+  return ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave;
+}
+
 // XCD-aware tile order. Consecutive workgroup ids are dispatched round-robin
 // over the 8 XCDs; remapping gives each XCD a contiguous run of logical tiles,
 // and the logical order walks groups of 8 tile-rows so that neighbours share
@@ -276,7 +292,8 @@ __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <class Op, MmaOut OUT>
-__global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
+__global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
+  const KParams p = batch_view(batch_p);
   // [stage][A | B][row * 8 + physical chunk], 16 bytes per entry: 128 KB.
   __shared__ __attribute__((aligned(1024))) i32x4 lds[2][2][kFastTile * kChunks];
 
@@ -486,7 +503,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams p) {
   column_block(IntC<2>{});
   column_block(IntC<3>{});
 
-  cycle_record(p.probe, t0, blockIdx.x * 4 + wave, wave);
+  cycle_record(p.probe, t0, probe_slot(wave), wave);
 }
 
 // ---------------------------------------------------------------------------
@@ -498,7 +515,8 @@ constexpr int kGenKBytes = 64;                 // two MFMA k-steps per stage
 constexpr int kGenRowBytes = kGenKBytes + 16;  // padded row: conflict-free b128 reads
 
 template <class Op, MmaOut OUT>
-__global__ __launch_bounds__(256) void gemm_general(KParams p) {
+__global__ __launch_bounds__(256) void gemm_general(KParams batch_p) {
+  const KParams p = batch_view(batch_p);
   constexpr int EB = Op::kElemBytes;
   constexpr int KT = kGenKBytes / EB;  // elements of K per stage
   __shared__ __attribute__((aligned(16))) uint8_t sa[kGenTile * kGenRowBytes];
@@ -571,7 +589,7 @@ __global__ __launch_bounds__(256) void gemm_general(KParams p) {
   }
 
   store_acc_tile<Op, OUT>(p, acc, row0 + wm * 32, col0 + wn * 32, lane);
-  cycle_record(p.probe, t0, blockIdx.x * 4 + wave, wave);
+  cycle_record(p.probe, t0, probe_slot(wave), wave);
 }
 
 // ---------------------------------------------------------------------------
@@ -591,6 +609,10 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   p.ialpha = d.ialpha; p.ibeta = d.ibeta;
   p.scale = d.scale;
   p.probe = d.probe;
+  constexpr int kOutBytes = (OUT == MmaOut::F32 || OUT == MmaOut::I32) ? 4 : 2;
+  p.sa = d.stride_a * Op::kElemBytes;
+  p.sb = d.stride_b * Op::kElemBytes;
+  p.sc = d.stride_c * kOutBytes;
 
   constexpr int EB = Op::kElemBytes;
   // The fast path needs K-contiguous operands whose rows start on 16-byte
@@ -604,19 +626,20 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
       (d.lda * EB) % 16 == 0 && (d.ldb * EB) % 16 == 0 &&
       ((uintptr_t)d.a % 16) == 0 && ((uintptr_t)d.b % 16) == 0 &&
       d.ldc % 8 == 0 && ((uintptr_t)d.c % 16) == 0 &&
+      p.sa % 16 == 0 && p.sb % 16 == 0 && p.sc % 16 == 0 &&
       (int64_t)kFastTile * d.lda * EB < (1ll << 31) &&
       (int64_t)kFastTile * d.ldb * EB < (1ll << 31);
   if (fast) {
     p.tiles_m = (d.m + kFastTile - 1) / kFastTile;
     p.tiles_n = (d.n + kFastTile - 1) / kFastTile;
     const int blocks = p.tiles_m * p.tiles_n;
-    hipLaunchKernelGGL((gemm_tn_fast<Op, OUT>), dim3(blocks), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tn_fast<Op, OUT>), dim3(blocks, d.batch), dim3(256), 0, s, p);
   } else {
     p.tiles_m = (d.m + kGenTile - 1) / kGenTile;
     p.tiles_n = (d.n + kGenTile - 1) / kGenTile;
     const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_general<Op, OUT>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_general<Op, OUT>), dim3((unsigned)blocks, d.batch), dim3(256), 0, s, p);
   }
   return hipGetLastError();
 }

@@ -31,6 +31,8 @@ struct GemmDesc {
   int32_t ialpha, ibeta;    // integer epilogue
   const float* scale;       // DEQ_BF16
   grxCycleSlot* probe;      // may be null
+  int batch = 1;            // grid.y; batch b offsets a, b, c by b * stride
+  int64_t stride_a = 0, stride_b = 0, stride_c = 0;  // elements, signed
 };
 
 // Picks the kernel (TN fast path or general path) and launches it.

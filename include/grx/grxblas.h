@@ -86,6 +86,28 @@ grxblasStatus_t grxblasGemmEx(grxblasHandle_t handle,
                               const float* beta,
                               void* C, grxDataType_t Ctype, int ldc);
 
+/* new: strided batch of GemmEx in one launch. No counterpart in the
+ * reference header: it joins grxblasGemmEx's type triples, alpha/beta rules
+ * and validation (ref grxblas.h:97-105, src/libs/grxblas/grxblas.cpp:507-584)
+ * with grxblasSgemmStridedBatched's batch convention (ref grxblas.h:207-212):
+ * batch b computes C + b*strideC from A + b*strideA and B + b*strideB;
+ * strides are signed, in elements, and a zero stride broadcasts A or B.
+ * batchCount == 0 is a successful no-op, a negative one INVALID_VALUE, more
+ * than 65535 NOT_SUPPORTED. With a cycle probe attached, the capacity must
+ * cover batchCount times the slots of one GemmEx of the same shape. */
+grxblasStatus_t grxblasGemmStridedBatchedEx(grxblasHandle_t handle,
+                                            grxblasOperation_t transa,
+                                            grxblasOperation_t transb,
+                                            int m, int n, int k,
+                                            const float* alpha,
+                                            const void* A, grxDataType_t Atype, int lda,
+                                            long long strideA,
+                                            const void* B, grxDataType_t Btype, int ldb,
+                                            long long strideB,
+                                            const float* beta,
+                                            void* C, grxDataType_t Ctype, int ldc,
+                                            long long strideC, int batchCount);
+
 /* new: int8 GEMM with per-output-channel dequantisation.
  *
  *   acc[i,j] = sum_l op(A)[i,l] * op(B)[l,j]                 (exact, int32)
