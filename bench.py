@@ -10,7 +10,9 @@ transb=N; fp32 accumulate, bf16 C), in TFLOP/s of algorithmic work
 The other BASELINE configs (bf16 4096^3, int8 GEMM + per-channel dequant,
 RMSNorm / LayerNorm, causal attention) are reported under "ops", each with its
 own roofline. Every kernel time is the HIP-event time of K back-to-back
-launches on the library handle's stream divided by K.
+launches on the library handle's stream divided by K, after W untimed
+launches (default: as many as fill 0.25 s, at least 10; each line reports
+its count as "warmup").
 
 The CPU baseline (rank 0, N=1) times the oracle -- the reference's own CPU
 GEMM loop restated in C (ref tests/libs/test_grxblas_ex.cpp:45-63) -- on a
@@ -41,9 +43,29 @@ def log(msg: str) -> None:
     sys.stderr.flush()
 
 
-def time_launches(stream: g.Stream, launch, steps: int, warmup: int) -> float:
-    """Mean milliseconds per launch over `steps` launches (after `warmup`),
-    measured with HIP events on the launching stream."""
+WARM_SECONDS = 0.25   # auto warm-up: at least this much back-to-back work
+LAST_WARMUP = [0]     # warm-up launches of the latest measurement
+
+
+def time_launches(stream: g.Stream, launch, steps: int, warmup: int | None) -> float:
+    """Mean milliseconds per launch over `steps` launches, measured with HIP
+    events on the launching stream, after `warmup` untimed launches. With
+    warmup None the count is chosen so that the warm-up runs for at least
+    WARM_SECONDS (and at least 10 launches): the GPU idles while the host
+    generates inputs, and a few launches after that sit in the clock ramp
+    (measured: 4-13 % slower with 10 warm-up launches of these kernels)."""
+    if warmup is None:
+        e0, e1 = g.Event(), g.Event()
+        e0.record(stream.s)
+        for _ in range(3):
+            launch()
+        e1.record(stream.s)
+        probe_ms = max(e0.elapsed_ms(e1) / 3, 1e-3)
+        g.synchronize()
+        e0.close()
+        e1.close()
+        warmup = max(10, int(np.ceil(WARM_SECONDS * 1e3 / probe_ms)))
+    LAST_WARMUP[0] = warmup
     for _ in range(warmup):
         launch()
     g.synchronize()
@@ -179,7 +201,8 @@ def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu):
     log(f"bf16 GemmEx {M}^3: timing")
     ms = time_launches(stream, launch, steps, warmup)
     flops = 2.0 * M * N * K
-    out = {"name": f"gemm_bf16_{M}", "ms": round(ms, 4), "value": round(flops / ms / 1e9, 2),
+    out = {"name": f"gemm_bf16_{M}", "ms": round(ms, 4), "warmup": LAST_WARMUP[0],
+           "value": round(flops / ms / 1e9, 2),
            "unit": "TFLOP/s", "roofline": roofline("mfma", flops, ms, "bf16", f"gemm_bf16_{M}")}
     if cpu:
         log("bf16 GemmEx: CPU baseline")
@@ -205,7 +228,8 @@ def bench_sgemm(stream, blas, steps, warmup):
     log("Sgemm 4096^3: timing")
     ms = time_launches(stream, launch, steps, warmup)
     flops = 2.0 * M * N * K
-    out = {"name": "sgemm_fp32_4096", "ms": round(ms, 4), "value": round(flops / ms / 1e9, 2),
+    out = {"name": "sgemm_fp32_4096", "ms": round(ms, 4), "warmup": LAST_WARMUP[0],
+           "value": round(flops / ms / 1e9, 2),
            "unit": "TFLOP/s", "roofline": roofline("mfma", flops, ms, "fp32", "sgemm_fp32_4096")}
     for d in (dA, dB, dC):
         d.close()
@@ -229,7 +253,7 @@ def bench_gemm_int8(stream, blas, steps, warmup, cpu):
     log("int8 GEMM + dequant: timing")
     ms = time_launches(stream, launch, steps, warmup)
     ops = 2.0 * M * N * K
-    out = {"name": "gemm_int8_dequant_4096x28672x8192", "ms": round(ms, 4),
+    out = {"name": "gemm_int8_dequant_4096x28672x8192", "ms": round(ms, 4), "warmup": LAST_WARMUP[0],
            "value": round(ops / ms / 1e9, 2), "unit": "TOP/s",
            "roofline": roofline("mfma", ops, ms, "int8", "gemm_int8_dequant")}
     if cpu:
@@ -265,7 +289,8 @@ def bench_norm(stream, dnn, layer, steps, warmup, cpu):
     log(f"{name}: timing")
     ms = time_launches(stream, launch, steps, warmup)
     moved = rows * hidden * 2 * 2 + hidden * 2 * (2 if layer else 1)
-    out = {"name": f"{name}_16384x8192", "ms": round(ms, 5), "value": round(moved / ms / 1e6, 1),
+    out = {"name": f"{name}_16384x8192", "ms": round(ms, 5), "warmup": LAST_WARMUP[0],
+           "value": round(moved / ms / 1e6, 1),
            "unit": "GB/s", "roofline": roofline("hbm", moved, ms, "hbm", name)}
     if cpu:
         out["cpu_baseline"] = cpu_norm_baseline(xs[0], gb, bb, rows, hidden, layer)
@@ -294,7 +319,8 @@ def bench_rowop(stream, dnn, op, steps, warmup):
     log(f"{op}: timing")
     ms = time_launches(stream, launch, steps, warmup)
     moved = rows * hidden * 2 * 2
-    out = {"name": f"{op}_16384x8192", "ms": round(ms, 5), "value": round(moved / ms / 1e6, 1),
+    out = {"name": f"{op}_16384x8192", "ms": round(ms, 5), "warmup": LAST_WARMUP[0],
+           "value": round(moved / ms / 1e6, 1),
            "unit": "GB/s", "roofline": roofline("hbm", moved, ms, "hbm", op)}
     for d in dx + dy:
         d.close()
@@ -318,7 +344,7 @@ def bench_attention(stream, dnn, steps, warmup, cpu):
     log("attention: timing")
     ms = time_launches(stream, launch, steps, warmup)
     flops = 4.0 * D * B * H * S * (S + 1) / 2
-    out = {"name": "attention_causal_b4h32s4096d128", "ms": round(ms, 4),
+    out = {"name": "attention_causal_b4h32s4096d128", "ms": round(ms, 4), "warmup": LAST_WARMUP[0],
            "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
            "roofline": roofline("mfma", flops, ms, "bf16", "attention")}
     if cpu:
@@ -336,7 +362,8 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed launches before each measurement (default: enough for %.2f s)" % WARM_SECONDS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention,sgemm,softmax,gelu")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
@@ -390,24 +417,26 @@ def main() -> int:
     if want("gelu"):
         ops.append(bench_rowop(stream, dnn, "gelu", args.steps, args.warmup))
 
-    if headline is None:
+    config = {"workload": "grxblasGemmEx bf16 M=N=K=8192, transa=T transb=N (row-major A x "
+                          "column-major B), fp32 accumulate, bf16 C, alpha=1 beta=0",
+              "m": 8192, "n": 8192, "k": 8192}
+    if headline is None:   # --only without gemm: the first op stands in
         headline = ops.pop(0)
+        config = {"workload": headline["name"]}
     line = {
         "metric": "GEMM/attention TFLOP/s (bf16, int8), RMSNorm GB/s; % of MI355X peak",
         "value": headline["value"],
         "unit": headline["unit"],
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": headline["warmup"],
         "ms_per_step": headline["ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1) bf16 (PCG64), resident in HBM before timing",
-        "config": {"workload": "grxblasGemmEx bf16 M=N=K=8192, transa=T transb=N (row-major A x "
-                               "column-major B), fp32 accumulate, bf16 C, alpha=1 beta=0",
-                   "m": 8192, "n": 8192, "k": 8192},
+        "config": config,
         "roofline": headline["roofline"],
         "cpu_baseline": headline.get("cpu_baseline"),
         "ops": ops,

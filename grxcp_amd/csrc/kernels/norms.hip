@@ -5,17 +5,19 @@
 // read once and every byte of y written once, so the design goal is streaming
 // bandwidth, not arithmetic.
 //
-//  * rows of up to 1024 16-byte chunks (8192 bf16): one row per 64-lane
+//  * rows of up to 256 16-byte chunks (2048 bf16): one row per 64-lane
 //    wavefront, held packed in registers between the statistics pass and the
 //    output pass; both statistics are shuffle reductions, so there is no LDS
 //    and no barrier and every wave streams independently;
-//  * longer rows (up to 2048 chunks): one row per 256-thread workgroup, with
-//    a 4-entry LDS combine; x is still read from HBM exactly once;
+//  * longer rows (up to 4096 chunks): one row per workgroup of chunks/2
+//    threads (256, 512 or 1024), two chunks per thread held in registers,
+//    one LDS combine per statistic; x is still read from HBM exactly once;
 //  * longer still: x re-read per pass (from L2);
 //  * 16-byte non-temporal loads of x and stores of y, gamma/beta via the
 //    normal cached path (every row reuses them);
-//  * statistics in fp32: wavefront butterfly (__shfl_xor) then a 4-entry LDS
-//    combine, summed in a fixed order so every thread sees the same value.
+//  * statistics in fp32: wavefront butterfly (__shfl_xor) then an LDS
+//    combine of the waves' partials, summed in a fixed order so every thread
+//    sees the same value.
 //    LayerNorm's variance is the two-pass (x - mean)^2 form over the cached
 //    registers, which costs no extra memory traffic.
 // Rows whose length, pitch or base alignment rule out 16-byte chunks take a
@@ -48,73 +50,90 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-template <NormType T, bool LAYER, int NQ>
-__global__ __launch_bounds__(256) void norm_vec(NParams p) {
+// One row per NT-thread workgroup, NQ 16-byte chunks per thread (chunk
+// tid + NT*q), for rows longer than a wavefront handles well. Measured on
+// 268 MB of bf16 rows: two chunks per thread with NT = chunks/2 streams at
+// 6.2-6.3 TB/s, against 5.6-5.8 TB/s for one row per wavefront at these
+// lengths. Each statistic is one wave butterfly plus one barrier; the waves'
+// partials are summed in a fixed order, so every thread sees the same value.
+template <NormType T, bool LAYER, int NT, int NQ>
+__global__ __launch_bounds__(NT) void norm_block(NParams p) {
   using IO = Io<T>;
   constexpr int V = IO::kVec;
-  __shared__ float red[4];
+  constexpr int NW = NT / 64;
+  __shared__ float red[2][NW];
   const int tid = threadIdx.x;
   const int nchunks = p.hidden / V;
   const float inv_h = 1.0f / (float)p.hidden;
+  auto combine = [&](float v, int slot) {
+    v = wave_sum(v);
+    if ((tid & 63) == 0) red[slot][tid >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t += red[slot][w];
+    return t;
+  };
 
   for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
     const uint8_t* xrow = p.x + row * p.x_rs * (int64_t)(16 / V);
     uint8_t* yrow = p.y + row * p.y_rs * (int64_t)(16 / V);
-
-    float v[NQ][V];
+    u32x4 raw[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = tid + NT * q;
+      raw[q] = c < nchunks ? __builtin_nontemporal_load((const u32x4*)xrow + c) : u32x4{0, 0, 0, 0};
+    }
     float s = 0.0f;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      const int c = tid + 256 * q;
-      if (c < nchunks) {
-        const u32x4 w = __builtin_nontemporal_load((const u32x4*)xrow + c);
-        IO::unpack(w, v[q]);
+      float v[V];
+      IO::unpack(raw[q], v);
 #pragma unroll
-        for (int e = 0; e < V; ++e) s += LAYER ? v[q][e] : v[q][e] * v[q][e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < V; ++e) v[q][e] = 0.0f;
-      }
+      for (int e = 0; e < V; ++e) s += LAYER ? v[e] : v[e] * v[e];
     }
-    s = block_sum(s, red);
+    s = combine(s, 0);
     float mean = 0.0f, inv;
     if (LAYER) {
       mean = s * inv_h;
       float d2 = 0.0f;
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
-        const int c = tid + 256 * q;
-        if (c < nchunks) {
+        if (tid + NT * q >= nchunks) continue;
+        float v[V];
+        IO::unpack(raw[q], v);
 #pragma unroll
-          for (int e = 0; e < V; ++e) {
-            const float d = v[q][e] - mean;
-            d2 += d * d;
-          }
+        for (int e = 0; e < V; ++e) {
+          const float d = v[e] - mean;
+          d2 += d * d;
         }
       }
-      d2 = block_sum(d2, red);
+      d2 = combine(d2, 1);
       inv = 1.0f / sqrtf(d2 * inv_h + p.eps);
     } else {
       inv = 1.0f / sqrtf(s * inv_h + p.eps);
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      const int c = tid + 256 * q;
-      if (c < nchunks) {
-        float g[V], o[V];
-        IO::unpack(((const u32x4*)p.gamma)[c], g);
-        if (LAYER) {
-          float b[V];
-          IO::unpack(((const u32x4*)p.beta)[c], b);
+      const int c = tid + NT * q;
+      if (c >= nchunks) continue;
+      float v[V], g[V], o[V];
+      IO::unpack(raw[q], v);
+      IO::unpack(((const u32x4*)p.gamma)[c], g);
+      if (LAYER) {
+        float b[V];
+        IO::unpack(((const u32x4*)p.beta)[c], b);
 #pragma unroll
-          for (int e = 0; e < V; ++e) o[e] = (v[q][e] - mean) * inv * g[e] + b[e];
-        } else {
+        for (int e = 0; e < V; ++e) o[e] = (v[e] - mean) * inv * g[e] + b[e];
+      } else {
 #pragma unroll
-          for (int e = 0; e < V; ++e) o[e] = v[q][e] * inv * g[e];
-        }
-        __builtin_nontemporal_store(IO::pack(o), (u32x4*)yrow + c);
+        for (int e = 0; e < V; ++e) o[e] = v[e] * inv * g[e];
       }
+      __builtin_nontemporal_store(IO::pack(o), (u32x4*)yrow + c);
     }
+    // Only a grid of fewer workgroups than rows (over 2^30 rows) loops: the
+    // next row's partials must not land before every wave has read these.
+    if (row + gridDim.x < p.rows) __syncthreads();
   }
 }
 
@@ -252,6 +271,7 @@ hipError_t run(const NormDesc& d, hipStream_t s) {
                    al(d.x) && al(d.y) && al(d.gamma) && (!LAYER || al(d.beta));
   const int nchunks = d.hidden / V;
   const unsigned wgrid = (unsigned)std::min<int64_t>((d.rows + 3) / 4, 1 << 30);
+  const unsigned bgrid = grid;
   if (vec && nchunks <= 64) {
     hipLaunchKernelGGL((norm_wave<T, LAYER, 1>), dim3(wgrid), dim3(256), 0, s, p);
   } else if (vec && nchunks <= 128) {
@@ -259,11 +279,13 @@ hipError_t run(const NormDesc& d, hipStream_t s) {
   } else if (vec && nchunks <= 256) {
     hipLaunchKernelGGL((norm_wave<T, LAYER, 4>), dim3(wgrid), dim3(256), 0, s, p);
   } else if (vec && nchunks <= 512) {
-    hipLaunchKernelGGL((norm_wave<T, LAYER, 8>), dim3(wgrid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((norm_block<T, LAYER, 256, 2>), dim3(bgrid), dim3(256), 0, s, p);
   } else if (vec && nchunks <= 1024) {
-    hipLaunchKernelGGL((norm_wave<T, LAYER, 16>), dim3(wgrid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((norm_block<T, LAYER, 512, 2>), dim3(bgrid), dim3(512), 0, s, p);
   } else if (vec && nchunks <= 2048) {
-    hipLaunchKernelGGL((norm_vec<T, LAYER, 8>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((norm_block<T, LAYER, 1024, 2>), dim3(bgrid), dim3(1024), 0, s, p);
+  } else if (vec && nchunks <= 4096) {
+    hipLaunchKernelGGL((norm_block<T, LAYER, 1024, 4>), dim3(bgrid), dim3(1024), 0, s, p);
   } else {
     hipLaunchKernelGGL((norm_scalar<T, LAYER>), dim3(grid), dim3(256), 0, s, p);
   }

@@ -93,6 +93,19 @@ def test_norm_other_types(dnn, t, layer):
 
 
 @pytest.mark.parametrize("layer", [False, True])
+@pytest.mark.parametrize("t,rows,hidden", [
+    (BF16, 5, 2056), (BF16, 7, 4104), (BF16, 3, 8200), (BF16, 3, 32768),   # ragged / full blocks
+    (F32, 6, 8192), (F32, 3, 3000), (F16, 4, 12000)])
+def test_norm_block_paths(dnn, t, layer, rows, hidden):
+    """Every workgroup-per-row configuration (256, 512, 1024 threads; two or
+    four chunks each), with row lengths that leave most of the last chunks
+    idle as well as ones that fill the block exactly."""
+    y, ref, _ = run_norm(dnn, layer, t, rows, hidden, seed=rows * hidden)
+    tol = {F32: 1e-5, F16: 2e-3, BF16: 1e-2}[t]
+    assert np.max(np.abs(y - ref)) <= tol * max(1.0, np.max(np.abs(ref)))
+
+
+@pytest.mark.parametrize("layer", [False, True])
 def test_norm_padded_rows(dnn, layer):
     y, ref, _ = run_norm(dnn, layer, BF16, 40, 1000, seed=9, pitch=1008)
     assert np.max(np.abs(y - ref)) <= 1e-2 * max(1.0, np.max(np.abs(ref)))
