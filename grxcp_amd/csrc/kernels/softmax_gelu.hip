@@ -4,13 +4,16 @@
 // docs/designs/grxcp_roadmap.md:864-877, grxcp_architecture.md:594) and ships
 // neither. Both are HBM-bound streams: x is read once and y written once.
 //
-// Softmax, rows of up to 1024 16-byte chunks: one row per wavefront, held
+// Softmax, rows of up to 256 16-byte chunks: one row per wavefront, held
 // packed in registers; the row max and the sum of exp(x - max) are shuffle
-// reductions (no LDS, no barrier); y = exp(x - max) / sum in fp32, rounded
-// once (16-bit outputs use the hardware exp2, fp32 the library expf). Longer or unaligned rows: one row per workgroup, three element-wise
-// passes (max, sum, write) re-reading x.
-// GELU: grid-stride over 16-byte chunks of every row (element-wise for
-// unaligned layouts), erf or tanh form in fp32, rounded once.
+// reductions (no LDS, no barrier). Up to 4096 chunks: one row per workgroup,
+// two or four chunks per thread in registers, one LDS combine per statistic.
+// y = exp(x - max) / sum in fp32, rounded once (16-bit outputs use the
+// hardware exp2, fp32 the library expf). Longer or unaligned rows: one row
+// per workgroup, three element-wise passes (max, sum, write) re-reading x.
+// GELU: one 16-byte chunk per thread, over the tensor as one array when its
+// rows are contiguous, else row by row (element-wise for unaligned layouts);
+// erf or tanh form in fp32, rounded once.
 
 #include "../launch.h"
 #include "device_common.h"
@@ -86,6 +89,75 @@ __global__ __launch_bounds__(256) void softmax_wave(RParams p) {
   }
 }
 
+// One row per NT-thread workgroup, NQ 16-byte chunks per thread (chunk
+// tid + NT*q), held in registers: the streaming layout that measured fastest
+// for rows of 2K-32K 16-bit elements (chunks/2 threads of two chunks each).
+// The row max and the sum are each a wave butterfly plus one LDS combine of
+// the waves' partials in a fixed order, identical in every thread.
+template <NormType T, int NT, int NQ>
+__global__ __launch_bounds__(NT) void softmax_block(RParams p) {
+  using IO = Io<T>;
+  constexpr int V = IO::kVec;
+  constexpr int NW = NT / 64;
+  __shared__ float red[2][NW];
+  const int tid = threadIdx.x;
+  const int nchunks = p.hidden / V;
+  for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
+    const uint8_t* xrow = p.x + row * p.x_rs * (int64_t)(16 / V);
+    uint8_t* yrow = p.y + row * p.y_rs * (int64_t)(16 / V);
+    u32x4 raw[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = tid + NT * q;
+      raw[q] = c < nchunks ? __builtin_nontemporal_load((const u32x4*)xrow + c) : u32x4{0, 0, 0, 0};
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if (tid + NT * q >= nchunks) continue;
+      float v[V];
+      IO::unpack(raw[q], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e) mx = fmaxf(mx, v[e]);
+    }
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[0][tid >> 6] = mx;
+    __syncthreads();
+    mx = red[0][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, red[0][w]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if (tid + NT * q >= nchunks) continue;
+      float v[V];
+      IO::unpack(raw[q], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e) sum += exp_le0<T>(v[e] - mx);
+    }
+    sum = wave_sum(sum);
+    if ((tid & 63) == 0) red[1][tid >> 6] = sum;
+    __syncthreads();
+    sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sum += red[1][w];
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = tid + NT * q;
+      if (c >= nchunks) continue;
+      float v[V], o[V];
+      IO::unpack(raw[q], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e) o[e] = exp_le0<T>(v[e] - mx) * inv;
+      __builtin_nontemporal_store(IO::pack(o), (u32x4*)yrow + c);
+    }
+    // Only a grid of fewer workgroups than rows (over 2^30 rows) loops: the
+    // next row's partials must not land before every wave has read these.
+    if (row + gridDim.x < p.rows) __syncthreads();
+  }
+}
+
 // Identical in every thread of the 256-thread workgroup.
 __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
   v = is_max ? wave_max(v) : wave_sum(v);
@@ -143,6 +215,24 @@ __global__ __launch_bounds__(256) void gelu_vec(RParams p) {
   }
 }
 
+// Contiguous rows (pitch == hidden): the tensor is one array of chunks, one
+// chunk per thread, no row arithmetic.
+template <NormType T, bool TANH>
+__global__ __launch_bounds__(256) void gelu_flat(RParams p) {
+  using IO = Io<T>;
+  constexpr int V = IO::kVec;
+  const int64_t total = p.rows * (int64_t)(p.hidden / V);
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    const u32x4 w = __builtin_nontemporal_load((const u32x4*)p.x + i);
+    float v[V];
+    IO::unpack(w, v);
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = gelu<TANH>(v[e]);
+    __builtin_nontemporal_store(IO::pack(v), (u32x4*)p.y + i);
+  }
+}
+
 template <NormType T, bool TANH>
 __global__ __launch_bounds__(256) void gelu_scalar(RParams p) {
   using IO = Io<T>;
@@ -179,14 +269,15 @@ hipError_t run_softmax(const RowDesc& d, hipStream_t s) {
   const int nchunks = d.hidden / Io<T>::kVec;
   const unsigned wgrid = (unsigned)std::min<int64_t>((d.rows + 3) / 4, 1 << 30);
   const bool vec = vec_layout<T>(d);
+  const unsigned bgrid = (unsigned)std::min<int64_t>(d.rows, 1 << 30);
   if (vec && nchunks <= 64) hipLaunchKernelGGL((softmax_wave<T, 1>), dim3(wgrid), dim3(256), 0, s, p);
   else if (vec && nchunks <= 128) hipLaunchKernelGGL((softmax_wave<T, 2>), dim3(wgrid), dim3(256), 0, s, p);
   else if (vec && nchunks <= 256) hipLaunchKernelGGL((softmax_wave<T, 4>), dim3(wgrid), dim3(256), 0, s, p);
-  else if (vec && nchunks <= 512) hipLaunchKernelGGL((softmax_wave<T, 8>), dim3(wgrid), dim3(256), 0, s, p);
-  else if (vec && nchunks <= 1024) hipLaunchKernelGGL((softmax_wave<T, 16>), dim3(wgrid), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((softmax_rows<T>), dim3((unsigned)std::min<int64_t>(d.rows, 1 << 30)), dim3(256),
-                       0, s, p);
+  else if (vec && nchunks <= 512) hipLaunchKernelGGL((softmax_block<T, 256, 2>), dim3(bgrid), dim3(256), 0, s, p);
+  else if (vec && nchunks <= 1024) hipLaunchKernelGGL((softmax_block<T, 512, 2>), dim3(bgrid), dim3(512), 0, s, p);
+  else if (vec && nchunks <= 2048) hipLaunchKernelGGL((softmax_block<T, 1024, 2>), dim3(bgrid), dim3(1024), 0, s, p);
+  else if (vec && nchunks <= 4096) hipLaunchKernelGGL((softmax_block<T, 1024, 4>), dim3(bgrid), dim3(1024), 0, s, p);
+  else hipLaunchKernelGGL((softmax_rows<T>), dim3(bgrid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
@@ -196,7 +287,9 @@ hipError_t run_gelu(const RowDesc& d, hipStream_t s) {
   const bool vec = vec_layout<T>(d);
   const int64_t items = vec ? d.rows * (d.hidden / Io<T>::kVec) : d.rows * d.hidden;
   const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((items + 255) / 256, 1 << 20));
-  if (vec) hipLaunchKernelGGL((gelu_vec<T, TANH>), dim3(grid), dim3(256), 0, s, p);
+  const bool flat = d.rows == 1 || (d.x_row_stride == d.hidden && d.y_row_stride == d.hidden);
+  if (vec && flat) hipLaunchKernelGGL((gelu_flat<T, TANH>), dim3(grid), dim3(256), 0, s, p);
+  else if (vec) hipLaunchKernelGGL((gelu_vec<T, TANH>), dim3(grid), dim3(256), 0, s, p);
   else hipLaunchKernelGGL((gelu_scalar<T, TANH>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }

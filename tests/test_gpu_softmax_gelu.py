@@ -52,8 +52,8 @@ def check(y, ref, t, atol=0.0):
     assert not bad.any(), (int(bad.sum()), float(err.max()))
 
 
-SOFTMAX_SHAPES = [(1, 1), (3, 7), (5, 64), (17, 1000), (64, 512), (8, 4096), (4, 8192),
-                  (3, 8200), (2, 32768), (2, 100003)]
+SOFTMAX_SHAPES = [(1, 1), (3, 7), (5, 64), (17, 1000), (64, 512), (5, 2056), (8, 4096), (4, 8192),
+                  (3, 8200), (3, 12000), (2, 32768), (2, 100003)]
 
 
 @pytest.mark.parametrize("t", [BF16, F16, F32])
@@ -81,12 +81,21 @@ def test_softmax_padded_rows_and_exact_cases(dnn):
     assert np.array_equal(y[0, :5], np.full(5, 0.2, np.float32)) and not y[0, 5:].any()
     assert np.isnan(y[1]).all()
     assert not y[2, ::2].any() and np.allclose(y[2, 1::2], 1.0 / 32, rtol=1e-6)
+    # the same special rows through the workgroup-per-row kernel
+    x = np.zeros((3, 4096), np.float32)
+    x[0, 5:] = -np.inf
+    x[1, :] = -np.inf
+    x[2, ::2] = -np.inf
+    y, _ = run_rows(dnn, "softmax", F32, x)
+    assert np.array_equal(y[0, :5], np.full(5, 0.2, np.float32)) and not y[0, 5:].any()
+    assert np.isnan(y[1]).all()
+    assert not y[2, ::2].any() and np.allclose(y[2, 1::2], 1.0 / 2048, rtol=1e-6)
 
 
 @pytest.mark.parametrize("mode", [g.GELU_ERF, g.GELU_TANH])
 @pytest.mark.parametrize("t", [BF16, F16, F32])
 @pytest.mark.parametrize("rows,hidden,pitch", [(1, 1, 1), (3, 7, 7), (5, 333, 340), (64, 4096, 4096),
-                                               (7, 1000, 1000), (1, 1 << 20, 1 << 20)])
+                                               (7, 1000, 1000), (6, 1024, 1040), (1, 1 << 20, 1 << 20)])
 def test_gelu_vs_oracle(dnn, mode, t, rows, hidden, pitch):
     x = (3.0 * np.random.default_rng(hidden + rows).standard_normal((rows, hidden))).astype(np.float32)
     y, ref = run_rows(dnn, "gelu", t, x, pitch=pitch, mode=mode)
