@@ -420,9 +420,12 @@ def main() -> int:
     config = {"workload": "grxblasGemmEx bf16 M=N=K=8192, transa=T transb=N (row-major A x "
                           "column-major B), fp32 accumulate, bf16 C, alpha=1 beta=0",
               "m": 8192, "n": 8192, "k": 8192}
+    dtype = "bf16"
     if headline is None:   # --only without gemm: the first op stands in
         headline = ops.pop(0)
         config = {"workload": headline["name"]}
+        dtype = ("f32" if headline["name"].startswith("sgemm") else
+                 "int8" if "int8" in headline["name"] else "bf16")
     line = {
         "metric": "GEMM/attention TFLOP/s (bf16, int8), RMSNorm GB/s; % of MI355X peak",
         "value": headline["value"],
@@ -434,7 +437,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": dtype,
         "data": "synthetic: seeded N(0,1) bf16 (PCG64), resident in HBM before timing",
         "config": config,
         "roofline": headline["roofline"],
