@@ -26,9 +26,22 @@
 #include "hip_status.h"
 #include "launch.h"
 
+// Device scratch for transposed operand copies (GemmEx layouts other than
+// T,N), one per device, grown on demand and kept until grxblasDestroy.
+// `done` is recorded after the last GEMM that read it; a call on another
+// stream waits for it before overwriting the copies.
+struct GemmWorkspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool used = false;
+};
+
 struct grxblasContext {
   hipStream_t stream = nullptr;
   std::mutex mutex;
+  std::array<GemmWorkspace, 64> ws{};
   std::string kernel_path;           // set by the first successful kernel lookup
   std::array<signed char, 64> device_ok{};  // per device: 0 unknown, 1 ok, -1 refused
   grxblasStatus_t device_status[64];
@@ -161,6 +174,65 @@ grxblasStatus_t probe_for(grxblasContext& ctx, int64_t needed, grxCycleSlot** ou
   return GRXBLAS_STATUS_SUCCESS;
 }
 
+// Give d the handle's workspace if the launch wants one (else the launch
+// takes the general path). Called with the context unlocked.
+hipError_t attach_workspace(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut out,
+                            grxk::GemmDesc& d, hipStream_t stream, GemmWorkspace** used) {
+  *used = nullptr;
+  const size_t need = grxk::gemm_workspace_bytes(in, out, d);
+  if (need == 0) return hipSuccess;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= (int)ctx.ws.size()) return hipSuccess;
+  std::lock_guard<std::mutex> lock(ctx.mutex);
+  GemmWorkspace& w = ctx.ws[dev];
+  if (w.bytes < need) {
+    if (w.ptr) {
+      // hipFree waits for the device, so no earlier GEMM still reads it.
+      (void)hipFree(w.ptr);
+      w.ptr = nullptr;
+      w.bytes = 0;
+    }
+    if (hipMalloc(&w.ptr, need) != hipSuccess) {
+      (void)hipGetLastError();
+      w.ptr = nullptr;
+      return hipSuccess;  // no workspace: general path
+    }
+    w.bytes = need;
+  }
+  if (!w.done && hipEventCreateWithFlags(&w.done, hipEventDisableTiming) != hipSuccess) {
+    w.done = nullptr;
+    return hipSuccess;
+  }
+  if (w.used && w.last != stream) {
+    const hipError_t e = hipStreamWaitEvent(stream, w.done, 0);
+    if (e != hipSuccess) return e;
+  }
+  d.ws = w.ptr;
+  d.ws_bytes = w.bytes;
+  *used = &w;
+  return hipSuccess;
+}
+
+// After a launch that read the workspace: mark where it ends.
+void release_workspace(grxblasContext& ctx, GemmWorkspace* w, hipStream_t stream) {
+  if (!w) return;
+  std::lock_guard<std::mutex> lock(ctx.mutex);
+  if (hipEventRecord(w->done, stream) == hipSuccess) {
+    w->last = stream;
+    w->used = true;
+  }
+}
+
+// One GemmEx-family launch with the workspace attached as needed.
+grxblasStatus_t launch_gemm(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut out,
+                            grxk::GemmDesc& d) {
+  GemmWorkspace* w = nullptr;
+  hipError_t e = attach_workspace(ctx, in, out, d, ctx.stream, &w);
+  if (e == hipSuccess) e = grxk::launch_mma_gemm(in, out, d, ctx.stream);
+  release_workspace(ctx, w, ctx.stream);
+  return from_hip(e);
+}
+
 // GemmEx and its strided batch. Validation order of ref
 // src/libs/grxblas/grxblas.cpp:507-524, the batch count checked where
 // SgemmStridedBatched checks it.
@@ -222,7 +294,7 @@ grxblasStatus_t gemm_ex_batched(grxblasHandle_t handle, grxblasOperation_t trans
   d.probe = probe;
   d.batch = batch;
   d.stride_a = strideA; d.stride_b = strideB; d.stride_c = strideC;
-  return from_hip(grxk::launch_mma_gemm(in, out, d, handle->stream));
+  return launch_gemm(*handle, in, out, d);
 }
 
 }  // namespace
@@ -254,6 +326,16 @@ grxblasStatus_t grxblasCreate(grxblasHandle_t* handle) {
 
 grxblasStatus_t grxblasDestroy(grxblasHandle_t handle) {
   if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
+  int cur = 0;
+  const bool have_cur = hipGetDevice(&cur) == hipSuccess;
+  for (int dev = 0; dev < (int)handle->ws.size(); ++dev) {
+    GemmWorkspace& w = handle->ws[dev];
+    if (!w.ptr && !w.done) continue;
+    if (hipSetDevice(dev) != hipSuccess) continue;
+    if (w.ptr) (void)hipFree(w.ptr);  // waits for the GEMMs that read it
+    if (w.done) (void)hipEventDestroy(w.done);
+  }
+  if (have_cur) (void)hipSetDevice(cur);
   delete handle;
   return GRXBLAS_STATUS_SUCCESS;
 }
@@ -363,8 +445,7 @@ grxblasStatus_t grxblasGemmExDequant(grxblasHandle_t handle, grxblasOperation_t 
   d.c = C; d.ldc = ldc;
   d.scale = scaleN;
   d.probe = probe;
-  return from_hip(grxk::launch_mma_gemm(grxk::MmaIn::I8, grxk::MmaOut::DEQ_BF16, d,
-                                        handle->stream));
+  return launch_gemm(*handle, grxk::MmaIn::I8, grxk::MmaOut::DEQ_BF16, d);
 }
 
 grxblasStatus_t grxblasSetCycleProbe(grxblasHandle_t handle, grxCycleSlot* slots, int capacity) {

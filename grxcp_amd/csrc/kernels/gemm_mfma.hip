@@ -593,55 +593,203 @@ __global__ __launch_bounds__(256) void gemm_general(KParams batch_p) {
 }
 
 // ---------------------------------------------------------------------------
+// operand transpose (for layouts the TN kernel cannot read directly)
+// ---------------------------------------------------------------------------
+
+// Y[c + r*ldy] = X[r + c*ldx] for r < R, c < C, elements of EB bytes; batch
+// blockIdx.z at X + z*sx, Y + z*sy (elements). 64x64-element tiles through
+// LDS: 16-byte loads along r, 16-byte stores along c. C is a multiple of
+// 16/EB (the caller's k), so an output chunk is wholly inside or outside.
+template <int EB>
+__global__ __launch_bounds__(256) void transpose_k(const uint8_t* X, int64_t ldx, int64_t sx,
+                                                   uint8_t* Y, int64_t ldy, int64_t sy, int R,
+                                                   int C, int vec_in) {
+  constexpr int T = 64;
+  constexpr int VE = 16 / EB;        // elements per 16-byte chunk
+  constexpr int CPS = T / VE;        // chunks per 64-element segment
+  constexpr int PITCH = T * EB + 16; // LDS bytes per c-row
+  __shared__ __attribute__((aligned(16))) uint8_t tile[T][PITCH];  // [c][r]
+  const int r0 = blockIdx.x * T, c0 = blockIdx.y * T;
+  X += (int64_t)blockIdx.z * sx * EB;
+  Y += (int64_t)blockIdx.z * sy * EB;
+  for (int q = threadIdx.x; q < T * CPS; q += 256) {
+    const int c = q / CPS, ch = q % CPS;
+    const int gc = c0 + c, gr = r0 + ch * VE;
+    uint8_t* dst = &tile[c][ch * 16];
+    const uint8_t* src = X + ((int64_t)gc * ldx + gr) * EB;
+    if (vec_in && gc < C && gr + VE <= R) {
+      *(u32x4*)dst = *(const u32x4*)src;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VE; ++e)
+#pragma unroll
+        for (int b = 0; b < EB; ++b) dst[e * EB + b] = (gc < C && gr + e < R) ? src[e * EB + b] : 0;
+    }
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < T * CPS; q += 256) {
+    const int r = q / CPS, ch = q % CPS;
+    const int gr = r0 + r, gc = c0 + ch * VE;
+    if (gr >= R || gc >= C) continue;
+    u32x4 w;
+    if constexpr (EB == 2) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        w[h] = (uint32_t)*(const uint16_t*)&tile[ch * VE + 2 * h][2 * r] |
+               ((uint32_t)*(const uint16_t*)&tile[ch * VE + 2 * h + 1][2 * r] << 16);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        w[h] = (uint32_t)tile[ch * VE + 4 * h][r] | ((uint32_t)tile[ch * VE + 4 * h + 1][r] << 8) |
+               ((uint32_t)tile[ch * VE + 4 * h + 2][r] << 16) |
+               ((uint32_t)tile[ch * VE + 4 * h + 3][r] << 24);
+    }
+    *(u32x4*)(Y + ((int64_t)gr * ldy + gc) * EB) = w;
+  }
+}
+
+template <int EB>
+hipError_t launch_transpose(const void* x, int64_t ldx, int64_t sx, void* y, int64_t ldy,
+                            int64_t sy, int R, int C, int batch, hipStream_t s) {
+  const int vec_in = ((uintptr_t)x % 16 == 0) && (ldx * EB) % 16 == 0 && (sx * EB) % 16 == 0;
+  const dim3 grid((unsigned)((R + 63) / 64), (unsigned)((C + 63) / 64), (unsigned)batch);
+  hipLaunchKernelGGL((transpose_k<EB>), grid, dim3(256), 0, s, (const uint8_t*)x, ldx, sx,
+                     (uint8_t*)y, ldy, sy, R, C, vec_in);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------
 
+constexpr int64_t kTransposeMinWork = 1ll << 25;  // m*n*k below this: general path
+
+template <MmaOut OUT>
+constexpr int out_bytes() { return (OUT == MmaOut::F32 || OUT == MmaOut::I32) ? 4 : 2; }
+
+// The TN kernel's requirements: K-contiguous operands whose rows start on
+// 16-byte boundaries (so every staged chunk is one aligned 16-byte load),
+// 32-bit buffer offsets within a 256-row panel, and a C whose columns start
+// on 16-byte boundaries (ldc % 8 == 0, aligned C), so that a run of 4 (32-bit)
+// or 8 (16-bit) rows of one column is one vector store.
+template <class Op, MmaOut OUT>
+bool tn_ready(const GemmDesc& d) {
+  constexpr int EB = Op::kElemBytes;
+  constexpr int OB = out_bytes<OUT>();
+  return d.ta && !d.tb && d.k > 0 && ((int64_t)d.k * EB) % 16 == 0 &&
+         (d.lda * EB) % 16 == 0 && (d.ldb * EB) % 16 == 0 &&
+         ((uintptr_t)d.a % 16) == 0 && ((uintptr_t)d.b % 16) == 0 &&
+         d.ldc % 8 == 0 && ((uintptr_t)d.c % 16) == 0 &&
+         (d.stride_a * EB) % 16 == 0 && (d.stride_b * EB) % 16 == 0 &&
+         (d.stride_c * OB) % 16 == 0 &&
+         (int64_t)kFastTile * d.lda * EB < (1ll << 31) &&
+         (int64_t)kFastTile * d.ldb * EB < (1ll << 31);
+}
+
+// Other layouts run the TN kernel behind K-contiguous copies of the operands
+// that are not: op(A) = A (transa N) is copied as A^T, op(B) = B^T (transb T)
+// as B. Worth it once the GEMM dwarfs the copy (one more read and write of
+// that operand); the copies sit back to back in the workspace.
+struct TPlan {
+  bool copy_a = false, copy_b = false;
+  int batch_a = 0, batch_b = 0;   // copies made (1 when the stride broadcasts)
+  size_t a_bytes = 0, b_bytes = 0;
+  GemmDesc e;                     // the TN problem over the copies (ws unset)
+};
+
+template <class Op, MmaOut OUT>
+bool plan_transposed(const GemmDesc& d, TPlan& t) {
+  constexpr int EB = Op::kElemBytes;
+  if (tn_ready<Op, OUT>(d)) return false;
+  if (d.k <= 0 || ((int64_t)d.k * EB) % 16 != 0) return false;
+  if ((int64_t)d.m * d.n * d.k < kTransposeMinWork) return false;
+  t = TPlan{};
+  t.copy_a = !d.ta;
+  t.copy_b = d.tb;
+  t.e = d;
+  t.e.ws = nullptr;
+  t.e.ws_bytes = 0;
+  auto round = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  if (t.copy_a) {
+    t.batch_a = d.stride_a == 0 ? 1 : d.batch;
+    t.a_bytes = round((size_t)t.batch_a * d.m * d.k * EB);
+    t.e.ta = true;
+    t.e.lda = d.k;
+    t.e.stride_a = d.stride_a == 0 ? 0 : (int64_t)d.m * d.k;
+  }
+  if (t.copy_b) {
+    t.batch_b = d.stride_b == 0 ? 1 : d.batch;
+    t.b_bytes = round((size_t)t.batch_b * d.n * d.k * EB);
+    t.e.tb = false;
+    t.e.ldb = d.k;
+    t.e.stride_b = d.stride_b == 0 ? 0 : (int64_t)d.n * d.k;
+  }
+  // The copies are 256-byte aligned, so only the kept operand and C decide.
+  GemmDesc probe = t.e;
+  if (t.copy_a) probe.a = (const void*)(uintptr_t)256;
+  if (t.copy_b) probe.b = (const void*)(uintptr_t)256;
+  return tn_ready<Op, OUT>(probe);
+}
+
 template <class Op, MmaOut OUT>
 hipError_t run(const GemmDesc& d, hipStream_t s) {
-  KParams p{};
-  p.a = (const uint8_t*)d.a;
-  p.b = (const uint8_t*)d.b;
-  p.c = d.c;
-  p.lda = d.lda; p.ldb = d.ldb; p.ldc = d.ldc;
-  p.m = d.m; p.n = d.n; p.k = d.k;
-  p.ta = d.ta; p.tb = d.tb;
-  p.alpha = d.alpha; p.beta = d.beta;
-  p.ialpha = d.ialpha; p.ibeta = d.ibeta;
-  p.scale = d.scale;
-  p.probe = d.probe;
-  constexpr int kOutBytes = (OUT == MmaOut::F32 || OUT == MmaOut::I32) ? 4 : 2;
-  p.sa = d.stride_a * Op::kElemBytes;
-  p.sb = d.stride_b * Op::kElemBytes;
-  p.sc = d.stride_c * kOutBytes;
-
   constexpr int EB = Op::kElemBytes;
-  // The fast path needs K-contiguous operands whose rows start on 16-byte
-  // boundaries (so every staged chunk is one aligned 16-byte load), 32-bit
-  // buffer offsets within a 256-row panel, and a C whose columns start on
-  // 16-byte boundaries (ldc % 8 == 0, aligned C), so that a run of 4 (32-bit)
-  // or 8 (16-bit) rows of one column is one vector store.
-  const bool fast =
-      d.ta && !d.tb && d.k > 0 &&
-      ((int64_t)d.k * EB) % 16 == 0 &&
-      (d.lda * EB) % 16 == 0 && (d.ldb * EB) % 16 == 0 &&
-      ((uintptr_t)d.a % 16) == 0 && ((uintptr_t)d.b % 16) == 0 &&
-      d.ldc % 8 == 0 && ((uintptr_t)d.c % 16) == 0 &&
-      p.sa % 16 == 0 && p.sb % 16 == 0 && p.sc % 16 == 0 &&
-      (int64_t)kFastTile * d.lda * EB < (1ll << 31) &&
-      (int64_t)kFastTile * d.ldb * EB < (1ll << 31);
-  if (fast) {
-    p.tiles_m = (d.m + kFastTile - 1) / kFastTile;
-    p.tiles_n = (d.n + kFastTile - 1) / kFastTile;
+  const GemmDesc* g = &d;
+  TPlan t;
+  if (plan_transposed<Op, OUT>(d, t) && d.ws && d.ws_bytes >= t.a_bytes + t.b_bytes) {
+    uint8_t* ws = (uint8_t*)d.ws;
+    if (t.copy_a) {
+      // A (m x k, m contiguous) -> A^T rows of k
+      const hipError_t e = launch_transpose<EB>(d.a, d.lda, d.stride_a, ws, d.k,
+                                                (int64_t)d.m * d.k, d.m, d.k, t.batch_a, s);
+      if (e != hipSuccess) return e;
+      t.e.a = ws;
+    }
+    if (t.copy_b) {
+      // B (n x k, n contiguous) -> rows of k per column j
+      const hipError_t e = launch_transpose<EB>(d.b, d.ldb, d.stride_b, ws + t.a_bytes, d.k,
+                                                (int64_t)d.n * d.k, d.n, d.k, t.batch_b, s);
+      if (e != hipSuccess) return e;
+      t.e.b = ws + t.a_bytes;
+    }
+    g = &t.e;
+  }
+
+  KParams p{};
+  p.a = (const uint8_t*)g->a;
+  p.b = (const uint8_t*)g->b;
+  p.c = g->c;
+  p.lda = g->lda; p.ldb = g->ldb; p.ldc = g->ldc;
+  p.m = g->m; p.n = g->n; p.k = g->k;
+  p.ta = g->ta; p.tb = g->tb;
+  p.alpha = g->alpha; p.beta = g->beta;
+  p.ialpha = g->ialpha; p.ibeta = g->ibeta;
+  p.scale = g->scale;
+  p.probe = g->probe;
+  p.sa = g->stride_a * EB;
+  p.sb = g->stride_b * EB;
+  p.sc = g->stride_c * out_bytes<OUT>();
+
+  if (tn_ready<Op, OUT>(*g)) {
+    p.tiles_m = (g->m + kFastTile - 1) / kFastTile;
+    p.tiles_n = (g->n + kFastTile - 1) / kFastTile;
     const int blocks = p.tiles_m * p.tiles_n;
-    hipLaunchKernelGGL((gemm_tn_fast<Op, OUT>), dim3(blocks, d.batch), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tn_fast<Op, OUT>), dim3(blocks, g->batch), dim3(256), 0, s, p);
   } else {
-    p.tiles_m = (d.m + kGenTile - 1) / kGenTile;
-    p.tiles_n = (d.n + kGenTile - 1) / kGenTile;
+    p.tiles_m = (g->m + kGenTile - 1) / kGenTile;
+    p.tiles_n = (g->n + kGenTile - 1) / kGenTile;
     const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_general<Op, OUT>), dim3((unsigned)blocks, d.batch), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_general<Op, OUT>), dim3((unsigned)blocks, g->batch), dim3(256), 0, s,
+                       p);
   }
   return hipGetLastError();
+}
+
+template <class Op, MmaOut OUT>
+size_t workspace(const GemmDesc& d) {
+  TPlan t;
+  return plan_transposed<Op, OUT>(d, t) ? t.a_bytes + t.b_bytes : 0;
 }
 
 }  // namespace
@@ -667,6 +815,24 @@ hipError_t launch_mma_gemm(MmaIn in, MmaOut out, const GemmDesc& d, hipStream_t 
       break;
   }
   return hipErrorNotSupported;
+}
+
+size_t gemm_workspace_bytes(MmaIn in, MmaOut out, const GemmDesc& d) {
+  switch (in) {
+    case MmaIn::BF16:
+      if (out == MmaOut::F32) return workspace<OpBF16, MmaOut::F32>(d);
+      if (out == MmaOut::BF16) return workspace<OpBF16, MmaOut::BF16>(d);
+      break;
+    case MmaIn::F16:
+      if (out == MmaOut::F32) return workspace<OpF16, MmaOut::F32>(d);
+      if (out == MmaOut::F16) return workspace<OpF16, MmaOut::F16>(d);
+      break;
+    case MmaIn::I8:
+      if (out == MmaOut::I32) return workspace<OpI8, MmaOut::I32>(d);
+      if (out == MmaOut::DEQ_BF16) return workspace<OpI8, MmaOut::DEQ_BF16>(d);
+      break;
+  }
+  return 0;
 }
 
 }  // namespace grxk

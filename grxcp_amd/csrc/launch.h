@@ -33,10 +33,16 @@ struct GemmDesc {
   grxCycleSlot* probe;      // may be null
   int batch = 1;            // grid.y; batch b offsets a, b, c by b * stride
   int64_t stride_a = 0, stride_b = 0, stride_c = 0;  // elements, signed
+  void* ws = nullptr;       // device workspace for transposed operand copies
+  size_t ws_bytes = 0;
 };
 
-// Picks the kernel (TN fast path or general path) and launches it.
+// Picks the kernel (TN fast path, TN fast path behind transposed copies of
+// the operands that are not K-contiguous, or the general path) and launches.
 hipError_t launch_mma_gemm(MmaIn in, MmaOut out, const GemmDesc& d, hipStream_t s);
+// Workspace bytes launch_mma_gemm would use for d (0: it needs none). With a
+// smaller d.ws_bytes the call takes the general path instead.
+size_t gemm_workspace_bytes(MmaIn in, MmaOut out, const GemmDesc& d);
 // Upper bound of probe slots any GEMM launch for an m x n output uses.
 int64_t gemm_probe_slots(int m, int n);
 

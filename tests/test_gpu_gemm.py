@@ -129,6 +129,52 @@ def test_fast_path_alpha_beta(blas):
     assert float_case(blas, F16, F16, 1, 0, 384, 320, 256, 2.5, -1.5, 8) == (0, 0)
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 1)])
+@pytest.mark.parametrize("in_t,out_t", [(BF16, BF16), (BF16, F32), (F16, F16), (F16, F32)])
+def test_transposed_copy_paths_exact(blas, in_t, out_t, ta, tb):
+    """Layouts other than T,N above the size threshold run the TN kernel behind
+    K-contiguous copies of op(A) / op(B) in the handle's workspace: ragged
+    shapes, padded leading dimensions, alpha/beta, still bit-exact."""
+    assert float_case(blas, in_t, out_t, ta, tb, 320, 264, 512, 1.0, 0.0, 0) == (0, 0)
+    assert float_case(blas, in_t, out_t, ta, tb, 264, 300, 520, 2.5, -1.5, 8) == (0, 0)
+
+
+def slots_written(blas, call, capacity):
+    """Run `call` with a zeroed cycle probe attached; count the slots written."""
+    import ctypes
+    slot_t = np.dtype([("start", np.uint64), ("end", np.uint64), ("core", np.uint32),
+                       ("warp", np.uint32)])
+    assert slot_t.itemsize == ctypes.sizeof(g.CycleSlot)
+    slots = to_dev(np.zeros(capacity, slot_t))
+    assert blas.set_cycle_probe(slots.p, capacity) == g.SUCCESS
+    try:
+        assert call() == g.SUCCESS
+        g.synchronize()
+    finally:
+        assert blas.set_cycle_probe(None, 0) == g.SUCCESS
+    got = slots.download(np.uint8, capacity * slot_t.itemsize).view(slot_t)
+    return int(np.count_nonzero(got["end"]))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 1), (1, 0)])
+def test_large_layouts_run_the_tn_kernel(blas, ta, tb):
+    """Every layout of a large GemmEx lands on the 256x256-tile kernel (one
+    probe slot per wave of its 2x2 tiles), not on the 64x64 general kernel
+    (100 slots for this shape)."""
+    m, n, k = 320, 264, 512
+    a_rows, a_cols = (k, m) if ta else (m, k)
+    b_rows, b_cols = (n, k) if tb else (k, n)
+    dA, dB = g.DeviceBuffer(a_rows * a_cols * 2), g.DeviceBuffer(b_rows * b_cols * 2)
+    dC = g.DeviceBuffer(m * n * 4)
+    call = lambda: blas.gemm_ex(ta, tb, m, n, k, 1.0, dA.p, BF16, a_rows, dB.p, BF16, b_rows,  # noqa: E731
+                                0.0, dC.p, F32, m)
+    assert slots_written(blas, call, blas.cycle_slots_needed(m, n)) == 4 * 2 * 2
+    # below the size threshold the general kernel runs
+    call = lambda: blas.gemm_ex(0, 0, 64, 64, 64, 1.0, dA.p, BF16, 64, dB.p, BF16, 64,  # noqa: E731
+                                0.0, dC.p, F32, 64)
+    assert slots_written(blas, call, blas.cycle_slots_needed(64, 64)) == 4
+
+
 def int8_case(blas, ta, tb, m, n, k, alpha, beta, pad, fill="ref", seed=0, cpad=None):
     """The reference's int8_case (ref test_grxblas_ex.cpp:254-322)."""
     kk = k if k else 1
@@ -170,6 +216,12 @@ def test_reference_int8_gate(blas):
 def test_int8_fast_path_exact(blas, m, n, k, pad, cpad):
     assert int8_case(blas, 1, 0, m, n, k, 1, 0, pad, fill="rand", seed=m + n + k, cpad=cpad) == 0
     assert int8_case(blas, 1, 0, m, n, k, 3, -2, pad, fill="rand", seed=m + n + k + 1, cpad=cpad) == 0
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 1)])
+def test_int8_transposed_copy_paths_exact(blas, ta, tb):
+    assert int8_case(blas, ta, tb, 300, 280, 512, 1, 0, 0, fill="rand", seed=7) == 0
+    assert int8_case(blas, ta, tb, 264, 256, 528, 3, -2, 16, fill="rand", seed=8, cpad=0) == 0
 
 
 def test_int8_refusals(blas):

@@ -111,6 +111,18 @@ def test_batched_int8_exact(blas, ta, tb, m, n, k):
                         seed=5) == 0
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 1)])
+def test_batched_transposed_copy_paths(blas, ta, tb):
+    """Large non-TN batches: per-batch operand copies (one copy when the
+    stride broadcasts), then the TN kernel."""
+    assert batched_case(blas, BF16, BF16, ta, tb, 256, 256, 512, 1.0, 0.0, 3, "packed", "neg",
+                        "gap") == 0
+    assert batched_case(blas, F16, F32, ta, tb, 256, 264, 512, 2.5, -1.5, 2, "zero", "zero",
+                        "packed", seed=4) == 0
+    assert batched_case(blas, I8, I32, ta, tb, 256, 256, 512, 2, 1, 2, "neg", "packed", "gap",
+                        seed=6) == 0
+
+
 def test_batched_attention_shape(blas):
     """Many small TN products in one launch (per-head score blocks): 32 batches
     of 256 x 256 x 128 bf16, each identical to its own GemmEx."""
