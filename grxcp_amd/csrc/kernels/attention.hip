@@ -4,9 +4,9 @@
 // (ref docs/designs/grxcp_roadmap.md:864-877). Single pass, online softmax,
 // O(S) memory:
 //
-//  * one workgroup = 4 wavefronts = 256 query rows of one (batch, head); each
-//    wave owns 64 queries (two 32-query blocks) whose Q fragments stay in
-//    VGPRs, so every K or V fragment read from LDS feeds two MFMAs;
+//  * one workgroup = 8 wavefronts (two per SIMD) = 256 query rows of one
+//    (batch, head); each wave owns 32 queries whose Q fragments stay in
+//    VGPRs for the whole pass;
 //  * K and V stream through LDS in 64-key tiles by direct-to-LDS buffer loads
 //    (no staging registers; rows past the sequence read as zero), double
 //    buffered, the next tile's loads in flight during the current tile;
@@ -24,8 +24,8 @@
 //  * P is packed with v_cvt_pk_bf16_f32 (round to nearest even); O is
 //    divided by the row sum once at the end and rounded once;
 //  * registers: this file is compiled with MFMA results in VGPRs
-//    (-amdgpu-mfma-vgpr-form) and Q parked in AGPRs, which keeps the scores,
-//    P and O out of AGPR<->VGPR copies;
+//    (-amdgpu-mfma-vgpr-form), which keeps the scores, P and O out of
+//    AGPR<->VGPR copies (184 VGPRs, two waves per SIMD);
 //  * causal: key tiles past the query tile are never loaded; a 32-query block
 //    skips tiles entirely above its diagonal; workgroups run heaviest first,
 //    and all query tiles of a head run on one XCD (K/V shared in its L2).
