@@ -264,6 +264,8 @@ def dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed):
 @pytest.mark.parametrize("ta,tb,m,n,k,pad,cpad", [
     (1, 0, 256, 256, 256, 0, 0), (1, 0, 300, 260, 528, 16, 4), (0, 0, 37, 29, 45, 3, 3),
     (1, 1, 33, 65, 77, 0, 0), (0, 1, 64, 64, 64, 0, 0), (1, 0, 5, 3, 0, 0, 0),
+    # above the size threshold: N,N / N,T / T,T through the transposed copies
+    (0, 0, 320, 264, 512, 0, 0), (0, 1, 256, 300, 528, 16, 8), (1, 1, 264, 256, 512, 0, 8),
 ])
 def test_dequant_bit_exact(blas, ta, tb, m, n, k, pad, cpad):
     assert dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed=m * 7 + n + k) == (0, 0)
