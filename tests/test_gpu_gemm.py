@@ -139,6 +139,37 @@ def test_transposed_copy_paths_exact(blas, in_t, out_t, ta, tb):
     assert float_case(blas, in_t, out_t, ta, tb, 264, 300, 520, 2.5, -1.5, 8) == (0, 0)
 
 
+def test_workspace_grows_and_follows_stream_changes():
+    """The transposed-copy workspace: a larger problem after a smaller one
+    (the workspace grows), and back-to-back calls alternating between two
+    streams with no host synchronisation in between (each call waits for the
+    previous user of the workspace). Every result bit-exact."""
+    blas = g.Blas()
+    streams = [g.Stream(), g.Stream()]
+    try:
+        cases = []
+        for i, (m, n, k) in enumerate([(256, 256, 512), (512, 384, 1024), (320, 512, 768),
+                                       (512, 512, 1024)]):
+            st = O.HalvesStream(100 + i)
+            A, B = st.take(m * k), st.take(k * n)     # N,N: A m x k (lda m), B k x n (ldb k)
+            hA, hB = narrow(A, BF16), narrow(B, BF16)
+            want = O.gemm_f32acc(0, 0, m, n, k, 1.0, A, m, B, k, 0.0, np.zeros(m * n, np.float32), m)
+            cases.append((m, n, k, to_dev(hA), to_dev(hB), g.DeviceBuffer(m * n * 4), want))
+        for i, (m, n, k, dA, dB, dC, _) in enumerate(cases):
+            blas.set_stream(streams[i % 2].s)
+            say(f"workspace case {i}: {m}x{n}x{k} on stream {i % 2}")
+            assert blas.gemm_ex(0, 0, m, n, k, 1.0, dA.p, BF16, m, dB.p, BF16, k, 0.0, dC.p, F32,
+                                m) == g.SUCCESS
+        g.synchronize()
+        for m, n, k, dA, dB, dC, want in cases:
+            got = dC.download(np.float32, m * n)
+            assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    finally:
+        blas.close()
+        for st in streams:
+            st.close()
+
+
 def slots_written(blas, call, capacity):
     """Run `call` with a zeroed cycle probe attached; count the slots written."""
     import ctypes
