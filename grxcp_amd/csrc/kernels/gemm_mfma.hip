@@ -31,6 +31,9 @@
 #include "../launch.h"
 #include "device_common.h"
 
+#include <algorithm>
+#include <type_traits>
+
 namespace grxk {
 namespace {
 
@@ -78,6 +81,7 @@ struct KParams {
   float alpha, beta;
   int32_t ialpha, ibeta;
   int64_t sa, sb, sc;     // batch strides in bytes (grid.y is the batch)
+  int k_last;             // split-K: k of the last grid.y slice (0: every slice has k)
   const float* scale;
   grxCycleSlot* probe;
 };
@@ -245,13 +249,16 @@ __device__ __forceinline__ int bits_of(T x) { return __builtin_bit_cast(int, x);
 template <class T>
 __device__ __forceinline__ T from_bits(int x) { return __builtin_bit_cast(T, x); }
 
-// The problem of batch blockIdx.y: operands and C moved by its strides.
+// The problem of batch blockIdx.y: operands and C moved by its strides. A
+// split-K launch uses the same mechanism: slice z reads K range
+// [z*k, (z+1)*k) (the last one k_last long) and writes its own partial C.
 __device__ __forceinline__ KParams batch_view(const KParams& in) {
   KParams p = in;
   const int64_t z = blockIdx.y;
   p.a += z * in.sa;
   p.b += z * in.sb;
   p.c = (uint8_t*)in.c + z * in.sc;
+  if (in.k_last && blockIdx.y == gridDim.y - 1) p.k = in.k_last;
   return p;
 }
 
@@ -659,6 +666,44 @@ hipError_t launch_transpose(const void* x, int64_t ldx, int64_t sx, void* y, int
 }
 
 // ---------------------------------------------------------------------------
+// split-K reduction
+// ---------------------------------------------------------------------------
+
+// C = epilogue(sum over s of W[s]), W[s] column-major with leading dimension
+// ldw (a multiple of 8, so every run is 16-byte aligned) and slice stride
+// sstride (elements). One thread per run of kRun rows of one column; slices
+// are summed in order s = 0, 1, ..., so the result does not depend on timing.
+// int32 partials add with two's complement wrap (unsigned arithmetic).
+template <MmaOut OUT, class E>
+__global__ __launch_bounds__(256) void reduce_splits(KParams p, const E* ws, int64_t ldw,
+                                                     int64_t sstride, int nsplit) {
+  constexpr int R = Epi<OUT>::kRun;
+  const int runs = (p.m + R - 1) / R;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)runs * p.n) return;
+  const int j = (int)(idx / runs);
+  const int i0 = (int)(idx % runs) * R;
+  E v[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) v[q] = 0;
+  for (int z = 0; z < nsplit; ++z) {
+    const E* src = ws + z * sstride + (int64_t)j * ldw + i0;
+#pragma unroll
+    for (int h = 0; h < R / 4; ++h) {
+      const i32x4 w = *(const i32x4*)(src + 4 * h);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if constexpr (std::is_integral<E>::value)
+          v[4 * h + q] = (E)((uint32_t)v[4 * h + q] + (uint32_t)w[q]);
+        else
+          v[4 * h + q] += from_bits<E>(w[q]);
+      }
+    }
+  }
+  store_run<OUT>(p, i0, j, v, R, true);
+}
+
+// ---------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------
 
@@ -689,71 +734,115 @@ bool tn_ready(const GemmDesc& d) {
 // Other layouts run the TN kernel behind K-contiguous copies of the operands
 // that are not: op(A) = A (transa N) is copied as A^T, op(B) = B^T (transb T)
 // as B. Worth it once the GEMM dwarfs the copy (one more read and write of
-// that operand); the copies sit back to back in the workspace.
-struct TPlan {
+// that operand). A TN problem too small to fill the GPU with 256x256 tiles
+// (fewer than kSplitTiles) and long in K is split along K: slice z computes
+// raw partials of its K range into the workspace (grid.y = slice) and
+// reduce_splits applies the epilogue to their sum. Workspace layout: copy of
+// A, copy of B, partials, each 256-byte aligned.
+constexpr int kSplitTiles = 128;
+constexpr int kMaxSplit = 16;
+
+struct Plan {
   bool copy_a = false, copy_b = false;
   int batch_a = 0, batch_b = 0;   // copies made (1 when the stride broadcasts)
   size_t a_bytes = 0, b_bytes = 0;
-  GemmDesc e;                     // the TN problem over the copies (ws unset)
+  int split = 1;                  // K slices
+  int kslice = 0, k_last = 0;     // elements
+  int64_t ldw = 0;                // partials' leading dimension
+  size_t w_bytes = 0;
+  bool tn = false;                // the TN kernel runs (directly or on copies)
+  GemmDesc e;                     // the TN problem (over the copies; ws unset)
+  size_t bytes() const { return a_bytes + b_bytes + w_bytes; }
 };
 
+inline size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
+
 template <class Op, MmaOut OUT>
-bool plan_transposed(const GemmDesc& d, TPlan& t) {
+Plan make_plan(const GemmDesc& d) {
   constexpr int EB = Op::kElemBytes;
-  if (tn_ready<Op, OUT>(d)) return false;
-  if (d.k <= 0 || ((int64_t)d.k * EB) % 16 != 0) return false;
-  if ((int64_t)d.m * d.n * d.k < kTransposeMinWork) return false;
-  t = TPlan{};
-  t.copy_a = !d.ta;
-  t.copy_b = d.tb;
+  Plan t;
   t.e = d;
   t.e.ws = nullptr;
   t.e.ws_bytes = 0;
-  auto round = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  if (t.copy_a) {
-    t.batch_a = d.stride_a == 0 ? 1 : d.batch;
-    t.a_bytes = round((size_t)t.batch_a * d.m * d.k * EB);
-    t.e.ta = true;
-    t.e.lda = d.k;
-    t.e.stride_a = d.stride_a == 0 ? 0 : (int64_t)d.m * d.k;
+  if (tn_ready<Op, OUT>(d)) {
+    t.tn = true;
+  } else if (d.k > 0 && ((int64_t)d.k * EB) % 16 == 0 &&
+             (int64_t)d.m * d.n * d.k >= kTransposeMinWork) {
+    Plan c = t;
+    c.copy_a = !d.ta;
+    c.copy_b = d.tb;
+    if (c.copy_a) {
+      c.batch_a = d.stride_a == 0 ? 1 : d.batch;
+      c.a_bytes = round256((size_t)c.batch_a * d.m * d.k * EB);
+      c.e.ta = true;
+      c.e.lda = d.k;
+      c.e.stride_a = d.stride_a == 0 ? 0 : (int64_t)d.m * d.k;
+    }
+    if (c.copy_b) {
+      c.batch_b = d.stride_b == 0 ? 1 : d.batch;
+      c.b_bytes = round256((size_t)c.batch_b * d.n * d.k * EB);
+      c.e.tb = false;
+      c.e.ldb = d.k;
+      c.e.stride_b = d.stride_b == 0 ? 0 : (int64_t)d.n * d.k;
+    }
+    // The copies are 256-byte aligned, so only the kept operand and C decide.
+    GemmDesc q = c.e;
+    if (c.copy_a) q.a = (const void*)(uintptr_t)256;
+    if (c.copy_b) q.b = (const void*)(uintptr_t)256;
+    if (tn_ready<Op, OUT>(q)) {
+      c.tn = true;
+      t = c;
+    }
   }
-  if (t.copy_b) {
-    t.batch_b = d.stride_b == 0 ? 1 : d.batch;
-    t.b_bytes = round((size_t)t.batch_b * d.n * d.k * EB);
-    t.e.tb = false;
-    t.e.ldb = d.k;
-    t.e.stride_b = d.stride_b == 0 ? 0 : (int64_t)d.n * d.k;
-  }
-  // The copies are 256-byte aligned, so only the kept operand and C decide.
-  GemmDesc probe = t.e;
-  if (t.copy_a) probe.a = (const void*)(uintptr_t)256;
-  if (t.copy_b) probe.b = (const void*)(uintptr_t)256;
-  return tn_ready<Op, OUT>(probe);
+  if (!t.tn || d.batch != 1 || d.probe) return t;
+  // Split K when the tiles leave most CUs idle (fewer than kSplitTiles), K has
+// at least 32 stages, and each slice keeps at least 8.
+  const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
+  const int64_t kbytes = (int64_t)d.k * EB;
+  if (tiles >= kSplitTiles || kbytes < 32 * kFastKBytes) return t;   // short K: not worth a second pass
+  int split = (int)std::min<int64_t>({(int64_t)kMaxSplit, 256 / tiles, kbytes / (8 * kFastKBytes)});
+  if (split < 2) return t;
+  const int unit = kFastKBytes / EB;                       // elements per stage
+  const int kslice = (int)((((int64_t)d.k + split - 1) / split + unit - 1) / unit) * unit;
+  split = (d.k + kslice - 1) / kslice;
+  if (split < 2) return t;
+  t.split = split;
+  t.kslice = kslice;
+  t.k_last = d.k - (split - 1) * kslice;
+  t.ldw = ((int64_t)d.m + 7) / 8 * 8;
+  t.w_bytes = round256((size_t)split * t.ldw * d.n * 4);
+  return t;
 }
 
 template <class Op, MmaOut OUT>
 hipError_t run(const GemmDesc& d, hipStream_t s) {
   constexpr int EB = Op::kElemBytes;
-  const GemmDesc* g = &d;
-  TPlan t;
-  if (plan_transposed<Op, OUT>(d, t) && d.ws && d.ws_bytes >= t.a_bytes + t.b_bytes) {
-    uint8_t* ws = (uint8_t*)d.ws;
-    if (t.copy_a) {
-      // A (m x k, m contiguous) -> A^T rows of k
-      const hipError_t e = launch_transpose<EB>(d.a, d.lda, d.stride_a, ws, d.k,
-                                                (int64_t)d.m * d.k, d.m, d.k, t.batch_a, s);
-      if (e != hipSuccess) return e;
-      t.e.a = ws;
-    }
-    if (t.copy_b) {
-      // B (n x k, n contiguous) -> rows of k per column j
-      const hipError_t e = launch_transpose<EB>(d.b, d.ldb, d.stride_b, ws + t.a_bytes, d.k,
-                                                (int64_t)d.n * d.k, d.n, d.k, t.batch_b, s);
-      if (e != hipSuccess) return e;
-      t.e.b = ws + t.a_bytes;
-    }
-    g = &t.e;
+  // The raw accumulator type of this input type, for split-K partials.
+  constexpr MmaOut RAW = std::is_same<Op, OpI8>::value ? MmaOut::I32 : MmaOut::F32;
+  using E = typename Op::Elem;
+  Plan t = make_plan<Op, OUT>(d);
+  if (t.bytes() > 0 && !(d.ws && d.ws_bytes >= t.bytes())) {
+    // No workspace for copies or partials: the kernel that fits d as it is.
+    t = Plan{};
+    t.e = d;
+    t.tn = tn_ready<Op, OUT>(d);
   }
+  uint8_t* ws = (uint8_t*)d.ws;
+  if (t.copy_a) {
+    // A (m x k, m contiguous) -> A^T rows of k
+    const hipError_t e = launch_transpose<EB>(d.a, d.lda, d.stride_a, ws, d.k,
+                                              (int64_t)d.m * d.k, d.m, d.k, t.batch_a, s);
+    if (e != hipSuccess) return e;
+    t.e.a = ws;
+  }
+  if (t.copy_b) {
+    // B (n x k, n contiguous) -> rows of k per column j
+    const hipError_t e = launch_transpose<EB>(d.b, d.ldb, d.stride_b, ws + t.a_bytes, d.k,
+                                              (int64_t)d.n * d.k, d.n, d.k, t.batch_b, s);
+    if (e != hipSuccess) return e;
+    t.e.b = ws + t.a_bytes;
+  }
+  const GemmDesc* g = &t.e;
 
   KParams p{};
   p.a = (const uint8_t*)g->a;
@@ -770,7 +859,29 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   p.sb = g->stride_b * EB;
   p.sc = g->stride_c * out_bytes<OUT>();
 
-  if (tn_ready<Op, OUT>(*g)) {
+  if (t.tn && t.split > 1) {
+    // Slices: raw partials into the workspace, then the epilogue over their sum.
+    KParams q = p;
+    E* w = (E*)(ws + t.a_bytes + t.b_bytes);
+    q.c = w;
+    q.ldc = t.ldw;
+    q.k = t.kslice;
+    q.k_last = t.k_last;
+    q.sa = (int64_t)t.kslice * EB;
+    q.sb = (int64_t)t.kslice * EB;
+    q.sc = t.ldw * g->n * 4;
+    q.alpha = 1.0f; q.beta = 0.0f; q.ialpha = 1; q.ibeta = 0;
+    q.scale = nullptr;
+    q.probe = nullptr;
+    q.tiles_m = (g->m + kFastTile - 1) / kFastTile;
+    q.tiles_n = (g->n + kFastTile - 1) / kFastTile;
+    hipLaunchKernelGGL((gemm_tn_fast<Op, RAW>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256), 0,
+                       s, q);
+    constexpr int R = Epi<OUT>::kRun;
+    const int64_t items = (int64_t)((g->m + R - 1) / R) * g->n;
+    hipLaunchKernelGGL((reduce_splits<OUT, E>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
+                       p, (const E*)w, t.ldw, t.ldw * g->n, t.split);
+  } else if (t.tn) {
     p.tiles_m = (g->m + kFastTile - 1) / kFastTile;
     p.tiles_n = (g->n + kFastTile - 1) / kFastTile;
     const int blocks = p.tiles_m * p.tiles_n;
@@ -788,8 +899,7 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
 
 template <class Op, MmaOut OUT>
 size_t workspace(const GemmDesc& d) {
-  TPlan t;
-  return plan_transposed<Op, OUT>(d, t) ? t.a_bytes + t.b_bytes : 0;
+  return make_plan<Op, OUT>(d).bytes();
 }
 
 }  // namespace

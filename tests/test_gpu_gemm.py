@@ -170,6 +170,48 @@ def test_workspace_grows_and_follows_stream_changes():
             st.close()
 
 
+@pytest.mark.parametrize("in_t,out_t", [(BF16, BF16), (BF16, F32), (F16, F16), (F16, F32)])
+@pytest.mark.parametrize("m,n,k,alpha,beta,pad,cpad", [
+    (1024, 1024, 8192, 1.0, 0.0, 0, 0),      # 16 tiles -> 16 K slices
+    (300, 520, 4160, 2.5, -1.5, 8, 4),       # ragged m/n, last slice shorter
+    (512, 2048, 2048, 1.0, 0.0, 0, 8),       # 16 tiles, 4 slices
+])
+def test_split_k_exact(blas, in_t, out_t, m, n, k, alpha, beta, pad, cpad):
+    """Problems with few 256x256 tiles and a long K are split along K; the
+    partial sums of exact inputs are exact, so the result stays bit-exact."""
+    assert float_case(blas, in_t, out_t, 1, 0, m, n, k, alpha, beta, pad, cpad) == (0, 0)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_split_k_after_transposed_copies(blas, ta, tb):
+    assert float_case(blas, BF16, BF16, ta, tb, 512, 256, 4096, 1.0, 0.0, 0) == (0, 0)
+
+
+def test_split_k_random_normal_tolerance(blas):
+    """1024 x 1024 x 8192 bf16 from N(0,1): split-K result within the
+    north-star bound of an fp64 reference."""
+    from grxcp_amd import synth
+    m = n = 1024
+    k = 8192
+    a = synth.normal_bf16(m * k, 5)            # A^T rows: k contiguous
+    b = synth.normal_bf16(n * k, 6)
+    dA, dB, dC = to_dev(a), to_dev(b), g.DeviceBuffer(m * n * 4)
+    say("split-k random normal 1024x1024x8192")
+    assert blas.gemm_ex(1, 0, m, n, k, 1.0, dA.p, BF16, k, dB.p, BF16, k, 0.0, dC.p, F32, m) == 0
+    g.synchronize()
+    got = dC.download(np.float32, m * n).reshape(n, m)
+    A = O.bf16_to_f32(a).reshape(m, k).astype(np.float64)
+    B = O.bf16_to_f32(b).reshape(n, k).astype(np.float64)
+    ref = B @ A.T                               # [n][m] = C column-major
+    assert normwise_rel_err(got.reshape(-1), ref.reshape(-1)) <= 1e-5
+
+
+def test_split_k_int8_and_dequant_exact(blas):
+    assert int8_case(blas, 1, 0, 1024, 512, 8192, 3, -2, 0, fill="rand", seed=21) == 0
+    assert int8_case(blas, 1, 0, 300, 260, 8320, 1, 1, 16, fill="rand", seed=22, cpad=4) == 0
+    assert dequant_case(blas, 1, 0, 512, 512, 8192, 0, 0, seed=23) == (0, 0)
+
+
 def slots_written(blas, call, capacity):
     """Run `call` with a zeroed cycle probe attached; count the slots written."""
     import ctypes
@@ -200,6 +242,11 @@ def test_large_layouts_run_the_tn_kernel(blas, ta, tb):
     call = lambda: blas.gemm_ex(ta, tb, m, n, k, 1.0, dA.p, BF16, a_rows, dB.p, BF16, b_rows,  # noqa: E731
                                 0.0, dC.p, F32, m)
     assert slots_written(blas, call, blas.cycle_slots_needed(m, n)) == 4 * 2 * 2
+    # a probe attached keeps a split-K candidate (few tiles, long K) unsplit
+    big = g.DeviceBuffer(256 * 8192 * 2)
+    call = lambda: blas.gemm_ex(1, 0, 256, 256, 8192, 1.0, big.p, BF16, 8192, big.p, BF16, 8192,  # noqa: E731
+                                0.0, dC.p, F32, 256)
+    assert slots_written(blas, call, blas.cycle_slots_needed(256, 256)) == 4
     # below the size threshold the general kernel runs
     call = lambda: blas.gemm_ex(0, 0, 64, 64, 64, 1.0, dA.p, BF16, 64, dB.p, BF16, 64,  # noqa: E731
                                 0.0, dC.p, F32, 64)
