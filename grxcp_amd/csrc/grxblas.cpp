@@ -27,21 +27,26 @@
 #include "launch.h"
 
 // Device scratch for transposed operand copies (GemmEx layouts other than
-// T,N), one per device, grown on demand and kept until grxblasDestroy.
-// `done` is recorded after the last GEMM that read it; a call on another
-// stream waits for it before overwriting the copies.
+// T,N) and split-K partial sums: one per (device, stream), grown on demand and
+// kept until grxblasDestroy. Stream order alone keeps two GEMMs from using
+// one workspace at once, so no event is recorded per call (an event record
+// costs ~2.5 us of GPU time, 10 % of a small split-K GEMM). A handle that
+// meets more than kStreamSlots streams on one device frees the least recently
+// used workspace (hipFree waits for the device) and gives it to the new one.
 struct GemmWorkspace {
   void* ptr = nullptr;
   size_t bytes = 0;
-  hipEvent_t done = nullptr;
-  hipStream_t last = nullptr;
-  bool used = false;
+  hipStream_t stream = nullptr;
+  uint64_t tick = 0;                // last use, for eviction
+  bool bound = false;               // stream is meaningful (0 is the null stream)
 };
+constexpr int kStreamSlots = 4;
 
 struct grxblasContext {
   hipStream_t stream = nullptr;
   std::mutex mutex;
-  std::array<GemmWorkspace, 64> ws{};
+  std::array<std::array<GemmWorkspace, kStreamSlots>, 64> ws{};
+  uint64_t ws_tick = 0;
   std::string kernel_path;           // set by the first successful kernel lookup
   std::array<signed char, 64> device_ok{};  // per device: 0 unknown, 1 ok, -1 refused
   grxblasStatus_t device_status[64];
@@ -174,62 +179,57 @@ grxblasStatus_t probe_for(grxblasContext& ctx, int64_t needed, grxCycleSlot** ou
   return GRXBLAS_STATUS_SUCCESS;
 }
 
-// Give d the handle's workspace if the launch wants one (else the launch
-// takes the general path). Called with the context unlocked.
-hipError_t attach_workspace(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut out,
-                            grxk::GemmDesc& d, hipStream_t stream, GemmWorkspace** used) {
-  *used = nullptr;
+// Give d the workspace of (current device, stream) if the launch wants one
+// (else the launch takes a path that needs none). Called with ctx.mutex held.
+hipError_t attach_workspace_locked(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut out,
+                                   grxk::GemmDesc& d, hipStream_t stream) {
   const size_t need = grxk::gemm_workspace_bytes(in, out, d);
   if (need == 0) return hipSuccess;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= (int)ctx.ws.size()) return hipSuccess;
-  std::lock_guard<std::mutex> lock(ctx.mutex);
-  GemmWorkspace& w = ctx.ws[dev];
-  if (w.bytes < need) {
-    if (w.ptr) {
-      // hipFree waits for the device, so no earlier GEMM still reads it.
-      (void)hipFree(w.ptr);
-      w.ptr = nullptr;
-      w.bytes = 0;
+  auto& slots = ctx.ws[dev];
+  GemmWorkspace* w = nullptr;
+  for (GemmWorkspace& c : slots)
+    if (c.bound && c.stream == stream) w = &c;
+  if (!w) {
+    for (GemmWorkspace& c : slots)
+      if (!w || !c.bound || (w->bound && c.tick < w->tick)) w = &c;
+    if (w->ptr) {
+      // hipFree waits for the device, so no GEMM on the old stream still uses it.
+      (void)hipFree(w->ptr);
+      w->ptr = nullptr;
+      w->bytes = 0;
     }
-    if (hipMalloc(&w.ptr, need) != hipSuccess) {
+    w->stream = stream;
+    w->bound = true;
+  }
+  w->tick = ++ctx.ws_tick;
+  if (w->bytes < need) {
+    if (w->ptr) {
+      (void)hipFree(w->ptr);
+      w->ptr = nullptr;
+      w->bytes = 0;
+    }
+    if (hipMalloc(&w->ptr, need) != hipSuccess) {
       (void)hipGetLastError();
-      w.ptr = nullptr;
-      return hipSuccess;  // no workspace: general path
+      w->ptr = nullptr;
+      return hipSuccess;  // no workspace: a path that needs none
     }
-    w.bytes = need;
+    w->bytes = need;
   }
-  if (!w.done && hipEventCreateWithFlags(&w.done, hipEventDisableTiming) != hipSuccess) {
-    w.done = nullptr;
-    return hipSuccess;
-  }
-  if (w.used && w.last != stream) {
-    const hipError_t e = hipStreamWaitEvent(stream, w.done, 0);
-    if (e != hipSuccess) return e;
-  }
-  d.ws = w.ptr;
-  d.ws_bytes = w.bytes;
-  *used = &w;
+  d.ws = w->ptr;
+  d.ws_bytes = w->bytes;
   return hipSuccess;
 }
 
-// After a launch that read the workspace: mark where it ends.
-void release_workspace(grxblasContext& ctx, GemmWorkspace* w, hipStream_t stream) {
-  if (!w) return;
-  std::lock_guard<std::mutex> lock(ctx.mutex);
-  if (hipEventRecord(w->done, stream) == hipSuccess) {
-    w->last = stream;
-    w->used = true;
-  }
-}
-
-// One GemmEx-family launch with the workspace attached as needed.
+// One GemmEx-family launch with the workspace attached as needed. The lock
+// spans attach and launch, so another thread on this handle cannot free or
+// regrow the workspace between the two.
 grxblasStatus_t launch_gemm(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut out,
                             grxk::GemmDesc& d) {
-  GemmWorkspace* w = nullptr;
-  hipError_t e = attach_workspace(ctx, in, out, d, ctx.stream, &w);
+  std::lock_guard<std::mutex> lock(ctx.mutex);
+  hipError_t e = attach_workspace_locked(ctx, in, out, d, ctx.stream);
   if (e == hipSuccess) e = grxk::launch_mma_gemm(in, out, d, ctx.stream);
-  release_workspace(ctx, w, ctx.stream);
   return from_hip(e);
 }
 
@@ -329,11 +329,11 @@ grxblasStatus_t grxblasDestroy(grxblasHandle_t handle) {
   int cur = 0;
   const bool have_cur = hipGetDevice(&cur) == hipSuccess;
   for (int dev = 0; dev < (int)handle->ws.size(); ++dev) {
-    GemmWorkspace& w = handle->ws[dev];
-    if (!w.ptr && !w.done) continue;
-    if (hipSetDevice(dev) != hipSuccess) continue;
-    if (w.ptr) (void)hipFree(w.ptr);  // waits for the GEMMs that read it
-    if (w.done) (void)hipEventDestroy(w.done);
+    for (GemmWorkspace& w : handle->ws[dev]) {
+      if (!w.ptr) continue;
+      if (hipSetDevice(dev) != hipSuccess) break;
+      (void)hipFree(w.ptr);  // waits for the GEMMs that read it
+    }
   }
   if (have_cur) (void)hipSetDevice(cur);
   delete handle;

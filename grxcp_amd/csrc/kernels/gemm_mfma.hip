@@ -32,6 +32,8 @@
 #include "device_common.h"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <type_traits>
 
 namespace grxk {
@@ -42,6 +44,7 @@ namespace {
 // ---------------------------------------------------------------------------
 
 struct OpBF16 {
+  static constexpr const char* kName = "bf16";
   using Acc = f32x16;
   using Elem = float;
   static constexpr int kElemBytes = 2;
@@ -52,6 +55,7 @@ struct OpBF16 {
 };
 
 struct OpF16 {
+  static constexpr const char* kName = "f16";
   using Acc = f32x16;
   using Elem = float;
   static constexpr int kElemBytes = 2;
@@ -62,6 +66,7 @@ struct OpF16 {
 };
 
 struct OpI8 {
+  static constexpr const char* kName = "i8";
   using Acc = i32x16;
   using Elem = int;
   static constexpr int kElemBytes = 1;
@@ -673,32 +678,50 @@ hipError_t launch_transpose(const void* x, int64_t ldx, int64_t sx, void* y, int
 // ldw (a multiple of 8, so every run is 16-byte aligned) and slice stride
 // sstride (elements). One thread per run of kRun rows of one column; slices
 // are summed in order s = 0, 1, ..., so the result does not depend on timing.
+// The loads of kBatch slices are issued before their adds (the sum is
+// latency-bound otherwise: few threads, one dependent HBM read per slice).
 // int32 partials add with two's complement wrap (unsigned arithmetic).
 template <MmaOut OUT, class E>
 __global__ __launch_bounds__(256) void reduce_splits(KParams p, const E* ws, int64_t ldw,
                                                      int64_t sstride, int nsplit) {
   constexpr int R = Epi<OUT>::kRun;
+  constexpr int H = R / 4;          // 16-byte loads per slice
+  constexpr int kBatch = 4;
   const int runs = (p.m + R - 1) / R;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)runs * p.n) return;
   const int j = (int)(idx / runs);
   const int i0 = (int)(idx % runs) * R;
+  const E* src = ws + (int64_t)j * ldw + i0;
   E v[R];
 #pragma unroll
   for (int q = 0; q < R; ++q) v[q] = 0;
-  for (int z = 0; z < nsplit; ++z) {
-    const E* src = ws + z * sstride + (int64_t)j * ldw + i0;
+  auto add = [&](const i32x4 (&w)[H]) {
 #pragma unroll
-    for (int h = 0; h < R / 4; ++h) {
-      const i32x4 w = *(const i32x4*)(src + 4 * h);
+    for (int h = 0; h < H; ++h)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         if constexpr (std::is_integral<E>::value)
-          v[4 * h + q] = (E)((uint32_t)v[4 * h + q] + (uint32_t)w[q]);
+          v[4 * h + q] = (E)((uint32_t)v[4 * h + q] + (uint32_t)w[h][q]);
         else
-          v[4 * h + q] += from_bits<E>(w[q]);
+          v[4 * h + q] += from_bits<E>(w[h][q]);
       }
-    }
+  };
+  int z = 0;
+  for (; z + kBatch <= nsplit; z += kBatch) {
+    i32x4 w[kBatch][H];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+      for (int h = 0; h < H; ++h) w[b][h] = *(const i32x4*)(src + (z + b) * sstride + 4 * h);
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) add(w[b]);
+  }
+  for (; z < nsplit; ++z) {
+    i32x4 w[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) w[h] = *(const i32x4*)(src + z * sstride + 4 * h);
+    add(w);
   }
   store_run<OUT>(p, i0, j, v, R, true);
 }
@@ -739,8 +762,9 @@ bool tn_ready(const GemmDesc& d) {
 // raw partials of its K range into the workspace (grid.y = slice) and
 // reduce_splits applies the epilogue to their sum. Workspace layout: copy of
 // A, copy of B, partials, each 256-byte aligned.
-constexpr int kSplitTiles = 128;
+constexpr int kSplitTiles = 256;
 constexpr int kMaxSplit = 16;
+constexpr int64_t kFixNs = 8000, kStageNs = 1030, kReduceNs = 6000, kPartialBytesPerNs = 10000;
 
 struct Plan {
   bool copy_a = false, copy_b = false;
@@ -795,23 +819,58 @@ Plan make_plan(const GemmDesc& d) {
     }
   }
   if (!t.tn || d.batch != 1 || d.probe) return t;
-  // Split K when the tiles leave most CUs idle (fewer than kSplitTiles), K has
-// at least 32 stages, and each slice keeps at least 8.
+  // Split K where a cost model (times in ns, fitted to kernel traces of
+  // 256x256 tiles at up to 256 workgroups) predicts at least 10 % less time.
+  // One pass: kFixNs (launch, prologue, epilogue) + kStageNs per 128-byte K
+  // stage. With s slices of at least 8 stages each (shorter slices measured
+  // slower than the model says: the K-loop's fill and drain dominate) and
+  // tiles * s <= 256 (one workgroup per CU), every workgroup runs
+  // ceil(stages/s) stages, plus the reduction: kReduceNs and the fp32
+  // partials written by the slices and read back, 8 * s * m * n bytes at
+  // kPartialBytesPerNs (mostly served from the last-level cache, hence above
+  // the HBM rate).
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
-  const int64_t kbytes = (int64_t)d.k * EB;
-  if (tiles >= kSplitTiles || kbytes < 32 * kFastKBytes) return t;   // short K: not worth a second pass
-  int split = (int)std::min<int64_t>({(int64_t)kMaxSplit, 256 / tiles, kbytes / (8 * kFastKBytes)});
-  if (split < 2) return t;
-  const int unit = kFastKBytes / EB;                       // elements per stage
-  const int kslice = (int)((((int64_t)d.k + split - 1) / split + unit - 1) / unit) * unit;
-  split = (d.k + kslice - 1) / kslice;
-  if (split < 2) return t;
+  const int64_t stages = ((int64_t)d.k * EB + kFastKBytes - 1) / kFastKBytes;
+  if (tiles >= kSplitTiles || stages < 16) return t;
+  const int64_t mn = ((int64_t)d.m + 7) / 8 * 8 * d.n;
+  auto cost = [&](int64_t sl, int64_t per) {
+    return kFixNs + kStageNs * per + (sl > 1 ? kReduceNs + 8 * sl * mn / kPartialBytesPerNs : 0);
+  };
+  const int64_t one = cost(1, stages);
+  int split = 1, per_best = (int)stages;
+  int64_t best = one;
+  for (int sl = 2; sl <= kMaxSplit && tiles * sl <= 256; ++sl) {
+    const int64_t per = (stages + sl - 1) / sl;
+    if (per < 8) break;
+    const int64_t slices = (stages + per - 1) / per;   // after rounding the slice up
+    const int64_t c = cost(slices, per);
+    if (c < best) {
+      best = c;
+      split = (int)slices;
+      per_best = (int)per;
+    }
+  }
+  if (split < 2 || best * 100 > one * 90) return t;
+  const int kslice = per_best * (kFastKBytes / EB);
   t.split = split;
   t.kslice = kslice;
   t.k_last = d.k - (split - 1) * kslice;
   t.ldw = ((int64_t)d.m + 7) / 8 * 8;
   t.w_bytes = round256((size_t)split * t.ldw * d.n * 4);
   return t;
+}
+
+// GRXBLAS_LOG set (and not "0"): one line on stderr per GemmEx-family call
+// naming the path it took. Read on every call, so it can be switched at run time.
+inline bool log_plans() {
+  const char* v = std::getenv("GRXBLAS_LOG");
+  return v && *v && !(v[0] == '0' && v[1] == 0);
+}
+
+template <MmaOut OUT>
+constexpr const char* out_name() {
+  return OUT == MmaOut::F32 ? "f32" : OUT == MmaOut::I32 ? "i32" : OUT == MmaOut::F16 ? "f16"
+       : OUT == MmaOut::BF16 ? "bf16" : "bf16(dequant)";
 }
 
 template <class Op, MmaOut OUT>
@@ -843,6 +902,13 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     t.e.b = ws + t.a_bytes;
   }
   const GemmDesc* g = &t.e;
+  if (log_plans()) {
+    std::fprintf(stderr,
+                 "grxblas: gemm %s->%s ta=%d tb=%d m=%d n=%d k=%d batch=%d kernel=%s copy_a=%d "
+                 "copy_b=%d split=%d\n",
+                 Op::kName, out_name<OUT>(), (int)d.ta, (int)d.tb, d.m, d.n, d.k, d.batch,
+                 t.tn ? "tn256" : "general64", (int)t.copy_a, (int)t.copy_b, t.split);
+  }
 
   KParams p{};
   p.a = (const uint8_t*)g->a;

@@ -9,6 +9,9 @@ library. int8 is integer and exact. Random-normal cases (the BASELINE config
 distributions) use the north-star bound: max relative error <= 1e-2 vs an
 fp32/fp64 reference.
 """
+import os
+import re
+
 import numpy as np
 import pytest
 
@@ -19,6 +22,19 @@ from helpers import col_major, from_col_major, normwise_rel_err, say, to_dev, wi
 pytestmark = pytest.mark.gpu
 
 F16, BF16, F32, I8, I32 = g.GRX_R_16F, g.GRX_R_16BF, g.GRX_R_32F, g.GRX_R_8I, g.GRX_R_32I
+
+
+def logged_plans(capfd, call):
+    """Run `call` with GRXBLAS_LOG=1; return the launch plans the library
+    printed, as dicts of the key=value fields of each line."""
+    capfd.readouterr()
+    os.environ["GRXBLAS_LOG"] = "1"
+    try:
+        call()
+    finally:
+        del os.environ["GRXBLAS_LOG"]
+    lines = [l for l in capfd.readouterr().err.splitlines() if l.startswith("grxblas: gemm ")]
+    return [dict(re.findall(r"(\w+)=(\w+)", l)) for l in lines]
 
 
 def narrow(vals: np.ndarray, t: int) -> np.ndarray:
@@ -142,8 +158,8 @@ def test_transposed_copy_paths_exact(blas, in_t, out_t, ta, tb):
 def test_workspace_grows_and_follows_stream_changes():
     """The transposed-copy workspace: a larger problem after a smaller one
     (the workspace grows), and back-to-back calls alternating between two
-    streams with no host synchronisation in between (each call waits for the
-    previous user of the workspace). Every result bit-exact."""
+    streams with no host synchronisation in between (each stream has its own
+    workspace). Every result bit-exact."""
     blas = g.Blas()
     streams = [g.Stream(), g.Stream()]
     try:
@@ -172,19 +188,79 @@ def test_workspace_grows_and_follows_stream_changes():
 
 @pytest.mark.parametrize("in_t,out_t", [(BF16, BF16), (BF16, F32), (F16, F16), (F16, F32)])
 @pytest.mark.parametrize("m,n,k,alpha,beta,pad,cpad", [
-    (1024, 1024, 8192, 1.0, 0.0, 0, 0),      # 16 tiles -> 16 K slices
+    (1024, 1024, 8192, 1.0, 0.0, 0, 0),      # 16 tiles, 128 stages
     (300, 520, 4160, 2.5, -1.5, 8, 4),       # ragged m/n, last slice shorter
-    (512, 2048, 2048, 1.0, 0.0, 0, 8),       # 16 tiles, 4 slices
+    (512, 2048, 2048, 1.0, 0.0, 0, 8),       # 16 tiles, 32 stages
 ])
-def test_split_k_exact(blas, in_t, out_t, m, n, k, alpha, beta, pad, cpad):
+def test_split_k_exact(blas, capfd, in_t, out_t, m, n, k, alpha, beta, pad, cpad):
     """Problems with few 256x256 tiles and a long K are split along K; the
     partial sums of exact inputs are exact, so the result stays bit-exact."""
-    assert float_case(blas, in_t, out_t, 1, 0, m, n, k, alpha, beta, pad, cpad) == (0, 0)
+    res = []
+    plans = logged_plans(capfd, lambda: res.append(
+        float_case(blas, in_t, out_t, 1, 0, m, n, k, alpha, beta, pad, cpad)))
+    assert res == [(0, 0)]
+    assert len(plans) == 1 and plans[0]["kernel"] == "tn256" and int(plans[0]["split"]) >= 2, plans
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
-def test_split_k_after_transposed_copies(blas, ta, tb):
-    assert float_case(blas, BF16, BF16, ta, tb, 512, 256, 4096, 1.0, 0.0, 0) == (0, 0)
+def test_split_k_after_transposed_copies(blas, capfd, ta, tb):
+    res = []
+    plans = logged_plans(capfd, lambda: res.append(
+        float_case(blas, BF16, BF16, ta, tb, 512, 256, 4096, 1.0, 0.0, 0)))
+    assert res == [(0, 0)]
+    p = plans[0]
+    assert (p["copy_a"], p["copy_b"]) == (str(1 - ta), str(tb)) and int(p["split"]) >= 2, plans
+
+
+def test_split_k_plan_limits(blas, capfd):
+    """Where the split does not pay: many tiles, short K, a batch."""
+    buf = g.DeviceBuffer(4096 * 4096 * 2)
+    out = g.DeviceBuffer(4096 * 4096 * 4)
+    calls = [
+        lambda: blas.gemm_ex(1, 0, 4096, 4096, 4096, 1.0, buf.p, BF16, 4096, buf.p, BF16, 4096,
+                             0.0, out.p, F32, 4096),                  # 256 tiles fill the CUs
+        lambda: blas.gemm_ex(1, 0, 1024, 1024, 512, 1.0, buf.p, BF16, 512, buf.p, BF16, 512,
+                             0.0, out.p, F32, 1024),                  # 8 stages
+        lambda: blas.gemm_strided_batched_ex(1, 0, 256, 256, 8192, 1.0, buf.p, BF16, 8192, 0,
+                                             buf.p, BF16, 8192, 0, 0.0, out.p, F32, 256,
+                                             256 * 256, 2),           # batch of 2
+        lambda: blas.gemm_ex(1, 0, 256, 256, 8192, 1.0, buf.p, BF16, 8192, buf.p, BF16, 8192,
+                             0.0, out.p, F32, 256),                   # the same, unbatched
+    ]
+    for want, call in zip(["1", "1", "1", "16"], calls):
+        plans = logged_plans(capfd, lambda: (call() == g.SUCCESS) or pytest.fail("call failed"))
+        g.synchronize()
+        assert [p["split"] for p in plans] == [want], plans
+
+
+def test_split_k_workspaces_on_many_streams():
+    """Split-K calls rotating over six streams (more than the handle keeps
+    workspaces for per device, so workspaces are handed over) with no host
+    synchronisation between calls. Every result bit-exact."""
+    blas = g.Blas()
+    streams = [g.Stream() for _ in range(6)]
+    try:
+        cases = []
+        for i in range(12):
+            m, n, k = 256 + 64 * (i % 3), 256, 4096 + 256 * (i % 2)
+            st = O.HalvesStream(200 + i)
+            A, B = st.take(m * k), st.take(k * n)     # T,N: A^T rows of k, B columns of k
+            hA, hB = narrow(A, BF16), narrow(B, BF16)
+            want = O.gemm_f32acc(1, 0, m, n, k, 1.0, A, k, B, k, 0.0, np.zeros(m * n, np.float32), m)
+            cases.append((m, n, k, to_dev(hA), to_dev(hB), g.DeviceBuffer(m * n * 4), want))
+        for i, (m, n, k, dA, dB, dC, _) in enumerate(cases):
+            blas.set_stream(streams[i % 6].s)
+            say(f"split-k stream case {i}: {m}x{n}x{k} on stream {i % 6}")
+            assert blas.gemm_ex(1, 0, m, n, k, 1.0, dA.p, BF16, k, dB.p, BF16, k, 0.0, dC.p, F32,
+                                m) == g.SUCCESS
+        g.synchronize()
+        for m, n, k, dA, dB, dC, want in cases:
+            got = dC.download(np.float32, m * n)
+            assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    finally:
+        blas.close()
+        for st in streams:
+            st.close()
 
 
 def test_split_k_random_normal_tolerance(blas):
@@ -206,10 +282,14 @@ def test_split_k_random_normal_tolerance(blas):
     assert normwise_rel_err(got.reshape(-1), ref.reshape(-1)) <= 1e-5
 
 
-def test_split_k_int8_and_dequant_exact(blas):
-    assert int8_case(blas, 1, 0, 1024, 512, 8192, 3, -2, 0, fill="rand", seed=21) == 0
-    assert int8_case(blas, 1, 0, 300, 260, 8320, 1, 1, 16, fill="rand", seed=22, cpad=4) == 0
-    assert dequant_case(blas, 1, 0, 512, 512, 8192, 0, 0, seed=23) == (0, 0)
+def test_split_k_int8_and_dequant_exact(blas, capfd):
+    res = []
+    plans = logged_plans(capfd, lambda: res.extend([
+        int8_case(blas, 1, 0, 1024, 512, 8192, 3, -2, 0, fill="rand", seed=21),
+        int8_case(blas, 1, 0, 300, 260, 8320, 1, 1, 16, fill="rand", seed=22, cpad=4),
+        dequant_case(blas, 1, 0, 512, 512, 8192, 0, 0, seed=23)]))
+    assert res == [0, 0, (0, 0)]
+    assert all(int(p["split"]) >= 2 for p in plans) and len(plans) == 3, plans
 
 
 def slots_written(blas, call, capacity):
