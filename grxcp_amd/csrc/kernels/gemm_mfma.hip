@@ -397,19 +397,23 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
     dma(kt, st, 4 * (d >> 3) + (d & 3), (d >> 2) & 1);
   };
 
-  // One k-step: 16 MFMAs on register set `buf`; behind every pair of MFMAs
-  // one fragment read for the next k-step and, in the phases that carry DMA,
-  // DMA instructions d0 .. d0+cnt-1 spread evenly over the 8 slots. The
-  // explicit order, held by sched_barrier, keeps the wave from stalling on a
-  // burst of DMA issues while its matrix core idles.
+  // One k-step: 16 MFMAs on register set `buf` in 8 slots of one MFMA pair.
+  // In the phases that carry DMA, DMA instructions d0 .. d0+cnt-1 are spread
+  // evenly over the slots, each issued ahead of its slot's MFMA pair: a DMA
+  // issue that waits for the address unit then waits while the previous
+  // pair still runs (measured 1-3 % faster than issuing it after the pair;
+  // moving the fragment read ahead as well is 3 % slower). Behind every pair
+  // one fragment read for the next k-step. The order is held by
+  // sched_barrier.
   auto phase = [&](int buf, int rd_st, int rd_ks, int dma_kt, int dma_st, int d0, int cnt) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int i = q >> 1, j0 = 2 * (q & 1);
+      if ((q + 1) * cnt / 8 > q * cnt / 8) dma_d(dma_kt, dma_st, d0 + q * cnt / 8);
+      __builtin_amdgcn_sched_barrier(0);
       acc[i][j0] = Op::mma(fa[buf][i], fb[buf][j0], acc[i][j0]);
       acc[i][j0 + 1] = Op::mma(fa[buf][i], fb[buf][j0 + 1], acc[i][j0 + 1]);
       frag(rd_st, rd_ks, buf ^ 1, q);
-      if ((q + 1) * cnt / 8 > q * cnt / 8) dma_d(dma_kt, dma_st, d0 + q * cnt / 8);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
