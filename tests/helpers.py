@@ -41,3 +41,31 @@ def normwise_rel_err(got: np.ndarray, ref: np.ndarray) -> float:
 
 def to_dev(a: np.ndarray) -> g.DeviceBuffer:
     return g.DeviceBuffer.from_array(a)
+
+
+GUARD = 4096
+POISON = 0xA5
+
+
+class Guarded:
+    """A device buffer holding `init`'s bytes between two 4 KB guard bands
+    filled with POISON: a kernel that writes outside its output changes
+    a guard band."""
+
+    def __init__(self, init: np.ndarray):
+        init = np.ascontiguousarray(init)
+        self.n = init.nbytes
+        self.buf = g.DeviceBuffer(self.n + 2 * GUARD)
+        self.buf.upload(np.full(self.n + 2 * GUARD, POISON, np.uint8))
+        self.buf.upload(init, offset=GUARD)
+        self.p = self.buf.ptr.value + GUARD
+
+    def download(self, dtype, count=None) -> np.ndarray:
+        if count is None:
+            count = self.n // np.dtype(dtype).itemsize
+        return self.buf.download(dtype, count, offset=GUARD)
+
+    def guards_intact(self) -> bool:
+        lo = self.buf.download(np.uint8, GUARD, offset=0)
+        hi = self.buf.download(np.uint8, GUARD, offset=GUARD + self.n)
+        return bool((lo == POISON).all() and (hi == POISON).all())

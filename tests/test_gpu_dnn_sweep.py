@@ -14,37 +14,13 @@ import pytest
 
 import grxcp_amd as g
 import oracle as O
-from helpers import normwise_rel_err, say, to_dev
+from helpers import Guarded, normwise_rel_err, say, to_dev
 from test_gpu_dnn import dec, enc, nptype
 from test_gpu_softmax_gelu import check
 
 pytestmark = pytest.mark.gpu
 
 BF16, F16, F32 = g.GRX_R_16BF, g.GRX_R_16F, g.GRX_R_32F
-GUARD = 4096
-POISON = 0xA5
-
-
-class Guarded:
-    """A device buffer of `init`'s bytes between two poisoned guard bands."""
-
-    def __init__(self, init: np.ndarray):
-        init = np.ascontiguousarray(init)
-        self.n = init.nbytes
-        self.buf = g.DeviceBuffer(self.n + 2 * GUARD)
-        self.buf.upload(np.full(self.n + 2 * GUARD, POISON, np.uint8))
-        self.buf.upload(init, offset=GUARD)
-        self.p = self.buf.ptr.value + GUARD
-
-    def body(self, dtype) -> np.ndarray:
-        return self.buf.download(dtype, self.n // np.dtype(dtype).itemsize, offset=GUARD)
-
-    def guards_intact(self) -> bool:
-        lo = self.buf.download(np.uint8, GUARD, offset=0)
-        hi = self.buf.download(np.uint8, GUARD, offset=GUARD + self.n)
-        return bool((lo == POISON).all() and (hi == POISON).all())
-
-
 def _pick(r, seq):
     return seq[int(r.integers(len(seq)))]
 
@@ -86,7 +62,7 @@ def test_norm_sweep(dnn):
              else dnn.rmsnorm(xd, dx.p, wd, dg.p, 1e-6, xd, dy.p))
         assert s == g.SUCCESS, g.STATUS[s]
         g.synchronize()
-        got = dy.body(nptype(t)).reshape(rows, pitch)
+        got = dy.download(nptype(t)).reshape(rows, pitch)
         y = dec(np.ascontiguousarray(got[:, :hidden]), t)
         gq, bq = dec(ge, t), dec(be, t)
         ref = O.layernorm(xq, gq, bq, 1e-6) if layer else O.rmsnorm(xq, gq, 1e-6)
@@ -115,7 +91,7 @@ def test_softmax_gelu_sweep(dnn):
         s = dnn.softmax(xd, dx.p, xd, dy.p) if op == "softmax" else dnn.gelu(mode, xd, dx.p, xd, dy.p)
         assert s == g.SUCCESS, g.STATUS[s]
         g.synchronize()
-        got = dy.body(nptype(t)).reshape(rows, pitch)
+        got = dy.download(nptype(t)).reshape(rows, pitch)
         y = dec(np.ascontiguousarray(got[:, :hidden]), t)
         ref = O.softmax(xq) if op == "softmax" else O.gelu(xq, mode).reshape(rows, hidden)
         try:
@@ -150,7 +126,7 @@ def test_attention_sweep(dnn):
         s = dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p)
         assert s == g.SUCCESS, g.STATUS[s]
         g.synchronize()
-        o = dec(do.body(np.uint16), t).reshape(shp)
+        o = dec(do.download(np.uint16), t).reshape(shp)
         qf, kf, vf = (dec(a, t).reshape(shp) for a in (q, k, v))
         ok = do.guards_intact()
         for b in range(B):

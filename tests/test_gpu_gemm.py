@@ -17,7 +17,7 @@ import pytest
 
 import grxcp_amd as g
 import oracle as O
-from helpers import col_major, from_col_major, normwise_rel_err, say, to_dev, window_mask
+from helpers import Guarded, col_major, from_col_major, normwise_rel_err, say, to_dev, window_mask
 
 pytestmark = pytest.mark.gpu
 
@@ -45,10 +45,12 @@ def widen(bits: np.ndarray, t: int) -> np.ndarray:
     return O.half_to_f32(bits) if t == F16 else O.bf16_to_f32(bits)
 
 
-def float_case(blas, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad=None, seed=99):
+def float_case(blas, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad=None, seed=99,
+               guard=False):
     """The reference's run_case (ref test_grxblas_ex.cpp:65-149), for any
     fp16/bf16 input and fp32/fp16/bf16 output. `pad` widens lda/ldb, `cpad`
-    (default: pad) widens ldc. Returns (#wrong, #stray)."""
+    (default: pad) widens ldc. With `guard`, C sits between guard bands and a
+    changed band counts as one stray write. Returns (#wrong, #stray)."""
     kk = k if k else 1
     a_rows, a_cols = (kk, m) if ta else (m, kk)
     b_rows, b_cols = (n, kk) if tb else (kk, n)
@@ -69,7 +71,8 @@ def float_case(blas, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad=None, 
         # the padding must come back as uploaded
         inside = window_mask(m, n, ldc)
         expected = np.where(inside, expected, c_host)
-    dA, dB, dC = to_dev(hA), to_dev(hB), to_dev(c_host)
+    dA, dB = to_dev(hA), to_dev(hB)
+    dC = Guarded(c_host) if guard else to_dev(c_host)
     say(f"gemm_ex in={in_t} out={out_t} ta={ta} tb={tb} {m}x{n}x{k} a={alpha} b={beta} pad={pad}")
     s = blas.gemm_ex(ta, tb, m, n, k, alpha, dA.p, in_t, lda, dB.p, in_t, ldb, beta, dC.p, out_t, ldc)
     assert s == g.SUCCESS, g.STATUS[s]
@@ -78,7 +81,8 @@ def float_case(blas, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad=None, 
     inside = window_mask(m, n, ldc)
     diff = got.view(np.uint32 if got.itemsize == 4 else np.uint16) != \
         expected.astype(c_host.dtype).view(np.uint32 if got.itemsize == 4 else np.uint16)
-    return int(np.sum(diff & inside)), int(np.sum(diff & ~inside))
+    stray = int(np.sum(diff & ~inside)) + (0 if not guard or dC.guards_intact() else 1)
+    return int(np.sum(diff & inside)), stray
 
 
 def gate_cases(tm, tn, tk):
@@ -333,8 +337,10 @@ def test_large_layouts_run_the_tn_kernel(blas, ta, tb):
     assert slots_written(blas, call, blas.cycle_slots_needed(64, 64)) == 4
 
 
-def int8_case(blas, ta, tb, m, n, k, alpha, beta, pad, fill="ref", seed=0, cpad=None):
-    """The reference's int8_case (ref test_grxblas_ex.cpp:254-322)."""
+def int8_case(blas, ta, tb, m, n, k, alpha, beta, pad, fill="ref", seed=0, cpad=None, guard=False):
+    """The reference's int8_case (ref test_grxblas_ex.cpp:254-322). With
+    `guard`, C sits between guard bands and a changed band counts as one
+    wrong element."""
     kk = k if k else 1
     a_rows, a_cols = (kk, m) if ta else (m, kk)
     b_rows, b_cols = (n, kk) if tb else (kk, n)
@@ -350,13 +356,14 @@ def int8_case(blas, ta, tb, m, n, k, alpha, beta, pad, fill="ref", seed=0, cpad=
         B = r.integers(-127, 128, ldb * b_cols).astype(np.int8)
         C = r.integers(-1000, 1000, ldc * n).astype(np.int32)
     want = O.igemm(ta, tb, m, n, k, int(alpha), A, lda, B, ldb, int(beta), C, ldc)
-    dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
+    dA, dB = to_dev(A), to_dev(B)
+    dC = Guarded(C) if guard else to_dev(C)
     say(f"igemm ta={ta} tb={tb} {m}x{n}x{k} a={alpha} b={beta} pad={pad}")
     s = blas.gemm_ex(ta, tb, m, n, k, alpha, dA.p, I8, lda, dB.p, I8, ldb, beta, dC.p, I32, ldc)
     assert s == g.SUCCESS, g.STATUS[s]
     g.synchronize()
     got = dC.download(np.int32, C.size)
-    return int(np.sum(got != want))
+    return int(np.sum(got != want)) + (0 if not guard or dC.guards_intact() else 1)
 
 
 def test_reference_int8_gate(blas):
@@ -397,7 +404,7 @@ def test_int8_refusals(blas):
     assert blas.gemm_ex_dequant(0, 0, 8, 4, 8, d.p, I8, 8, d.p, I8, 8, d.p, d.p, F32, 8) == g.NOT_SUPPORTED
 
 
-def dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed):
+def dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed, guard=False):
     kk = k if k else 1
     a_rows, a_cols = (kk, m) if ta else (m, kk)
     b_rows, b_cols = (n, kk) if tb else (kk, n)
@@ -409,14 +416,16 @@ def dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed):
     acc = O.igemm(ta, tb, m, n, k, 1, A, lda, B, ldb, 0, np.zeros(m * n, np.int32), m)
     want = O.dequant(m, n, acc, m, scale, ldc)
     poison = np.full(ldc * n, 0x7FC1, np.uint16)
-    dA, dB, dS, dC = to_dev(A), to_dev(B), to_dev(scale), to_dev(poison)
+    dA, dB, dS = to_dev(A), to_dev(B), to_dev(scale)
+    dC = Guarded(poison) if guard else to_dev(poison)
     say(f"dequant ta={ta} tb={tb} {m}x{n}x{k} pad={pad}")
     s = blas.gemm_ex_dequant(ta, tb, m, n, k, dA.p, I8, lda, dB.p, I8, ldb, dS.p, dC.p, BF16, ldc)
     assert s == g.SUCCESS, g.STATUS[s]
     g.synchronize()
     got = dC.download(np.uint16, ldc * n)
     inside = window_mask(m, n, ldc)
-    return int(np.sum((got != want) & inside)), int(np.sum((got != poison) & ~inside))
+    stray = int(np.sum((got != poison) & ~inside)) + (0 if not guard or dC.guards_intact() else 1)
+    return int(np.sum((got != want) & inside)), stray
 
 
 @pytest.mark.parametrize("ta,tb,m,n,k,pad,cpad", [

@@ -8,7 +8,8 @@ some cases take the 256x256-tile kernel directly, some through transposed
 operand copies, some split along K and some the general kernel. Inputs are
 exact by construction (the reference's method, ref
 tests/libs/test_grxblas_ex.cpp:1-14), so every case is compared BIT-EXACT
-over the whole padded C buffer against the CPU oracle. The path each call
+over the whole padded C buffer against the CPU oracle, with 4 KB guard
+bands on both sides of C that must come back unchanged. The path each call
 took is read from the library's GRXBLAS_LOG line, and each test asserts that
 its cases covered every path.
 """
@@ -69,7 +70,8 @@ def test_float_sweep(blas, capfd):
         beta = _pick(r, [0.0, 1.0, -1.5])
         res = []
         got = logged_plans(capfd, lambda: res.append(
-            float_case(blas, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad, seed=1000 + i)))
+            float_case(blas, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad, seed=1000 + i,
+                       guard=True)))
         plans += got
         if res != [(0, 0)]:
             bad.append((i, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad, res, got))
@@ -88,7 +90,8 @@ def test_int8_sweep(blas, capfd):
         beta = _pick(r, [0.0, 1.0, -1.0])
         res = []
         got = logged_plans(capfd, lambda: res.append(
-            int8_case(blas, ta, tb, m, n, k, alpha, beta, pad, fill="rand", seed=2000 + i, cpad=cpad)))
+            int8_case(blas, ta, tb, m, n, k, alpha, beta, pad, fill="rand", seed=2000 + i, cpad=cpad,
+                      guard=True)))
         plans += got
         if res != [0]:
             bad.append((i, ta, tb, m, n, k, alpha, beta, pad, cpad, res, got))
@@ -105,7 +108,7 @@ def test_dequant_sweep(blas, capfd):
         ta, tb, m, n, k, pad, cpad = _shape(r, kinds[i % 4], 1)
         res = []
         got = logged_plans(capfd, lambda: res.append(
-            dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed=3000 + i)))
+            dequant_case(blas, ta, tb, m, n, k, pad, cpad, seed=3000 + i, guard=True)))
         plans += got
         if res != [(0, 0)]:
             bad.append((i, ta, tb, m, n, k, pad, cpad, res, got))
