@@ -342,19 +342,43 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
   // the tile, and nothing waits for the data until the stage's barrier.
   const int lr = lane >> 3;
   const int pc = lane & 7;
-  // One DMA instruction: 1 KB (8 rows) of operand `op` for stage kt.
-  auto dma = [&](int kt, int st, int i, int op) {
+  // The stage-invariant part of each DMA's offset (row and swizzled chunk),
+  // per 8-row block group i and operand. A stage that lies wholly inside K
+  // needs no mask: its DMAs pass this offset and the stage's K offset in
+  // the instruction's scalar soffset, so the K loop spends no VALU
+  // instruction on DMA addresses (measured 2-3 % faster than recomputing and
+  // masking every offset per stage).
+  uint32_t base_a[8], base_b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int blk = 4 * i + wave;
+    const int row = 8 * blk + lr;
+    const int c = pc ^ lr ^ (blk & 7);
+    base_a[i] = (uint32_t)(row * lda_b + 16 * c);
+    base_b[i] = (uint32_t)(row * ldb_b + 16 * c);
+  }
+  // One DMA instruction: 1 KB (8 rows) of operand `op` for stage kt. `full`
+  // (compile-time) says the stage lies wholly inside K. Rows past m/n read
+  // zero either way: their stage-invariant offset alone is past the
+  // descriptor's record count.
+  auto dma = [&](int kt, int st, int i, int op, auto full) {
     const int kb = kt * kFastKBytes;
     const int blk = 4 * i + wave;               // 8-row block index, 0..31
-    const int row = 8 * blk + lr;
-    const int c = pc ^ lr ^ (blk & 7);          // == pc ^ swz(row)
-    const bool ok = kt < ktiles && kb + 16 * c < kbytes;
-    if (op == 0) {
-      const uint32_t va = ok ? (uint32_t)(row * lda_b + 16 * c + kb) : kOff;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&lds[st][0][blk * 64], 16, va, 0, 0, 0);
+    if constexpr (decltype(full)::value) {
+      if (op == 0)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&lds[st][0][blk * 64], 16, base_a[i], kb, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&lds[st][1][blk * 64], 16, base_b[i], kb, 0, 0);
     } else {
-      const uint32_t vb = ok ? (uint32_t)(row * ldb_b + 16 * c + kb) : kOff;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&lds[st][1][blk * 64], 16, vb, 0, 0, 0);
+      const int c = pc ^ lr ^ (blk & 7);          // == pc ^ swz(row)
+      const bool ok = kt < ktiles && kb + 16 * c < kbytes;
+      if (op == 0) {
+        const uint32_t va = ok ? base_a[i] + (uint32_t)kb : kOff;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&lds[st][0][blk * 64], 16, va, 0, 0, 0);
+      } else {
+        const uint32_t vb = ok ? base_b[i] + (uint32_t)kb : kOff;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&lds[st][1][blk * 64], 16, vb, 0, 0, 0);
+      }
     }
   };
 
@@ -393,8 +417,8 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
 
   // A stage is 16 DMA instructions, d = 0..15: 8-row block group
   // 4*(d/8) + d%4 of operand (d/4)%2.
-  auto dma_d = [&](int kt, int st, int d) {
-    dma(kt, st, 4 * (d >> 3) + (d & 3), (d >> 2) & 1);
+  auto dma_d = [&](int kt, int st, int d, auto full) {
+    dma(kt, st, 4 * (d >> 3) + (d & 3), (d >> 2) & 1, full);
   };
 
   // One k-step: 16 MFMAs on register set `buf` in 8 slots of one MFMA pair.
@@ -405,11 +429,11 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
   // moving the fragment read ahead as well is 3 % slower). Behind every pair
   // one fragment read for the next k-step. The order is held by
   // sched_barrier.
-  auto phase = [&](int buf, int rd_st, int rd_ks, int dma_kt, int dma_st, int d0, int cnt) {
+  auto phase = [&](int buf, int rd_st, int rd_ks, int dma_kt, int dma_st, int d0, int cnt, auto full) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int i = q >> 1, j0 = 2 * (q & 1);
-      if ((q + 1) * cnt / 8 > q * cnt / 8) dma_d(dma_kt, dma_st, d0 + q * cnt / 8);
+      if ((q + 1) * cnt / 8 > q * cnt / 8) dma_d(dma_kt, dma_st, d0 + q * cnt / 8, full);
       __builtin_amdgcn_sched_barrier(0);
       acc[i][j0] = Op::mma(fa[buf][i], fb[buf][j0], acc[i][j0]);
       acc[i][j0 + 1] = Op::mma(fa[buf][i], fb[buf][j0 + 1], acc[i][j0 + 1]);
@@ -427,23 +451,29 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
   // than the late loads then cost at the barrier.)
   constexpr int kDmaD = 8, kDmaA = 8;
 #pragma unroll
-  for (int d = 0; d < 16; ++d) dma_d(0, 0, d);
+  for (int d = 0; d < 16; ++d) dma_d(0, 0, d, std::false_type{});
 #pragma unroll
-  for (int d = 0; d < kDmaD; ++d) dma_d(1, 1, d);
+  for (int d = 0; d < kDmaD; ++d) dma_d(1, 1, d, std::false_type{});
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaD) : "memory");  // stage 0 landed
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < 8; ++q) frag(0, 0, 0, q);
 
-  for (int kt = 0; kt < ktiles; ++kt) {
+  auto iter = [&](int kt, auto full) __attribute__((always_inline)) {
     const int cur = kt & 1;
-    phase(0, cur, 1, kt + 1, cur ^ 1, kDmaD, kDmaA);
-    phase(1, cur, 2, 0, 0, 0, 0);
-    phase(0, cur, 3, 0, 0, 0, 0);
+    phase(0, cur, 1, kt + 1, cur ^ 1, kDmaD, kDmaA, full);
+    phase(1, cur, 2, 0, 0, 0, 0, full);
+    phase(0, cur, 3, 0, 0, 0, 0, full);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 landed
     __syncthreads();
-    phase(1, cur ^ 1, 0, kt + 2, cur, 0, kDmaD);
-  }
+    phase(1, cur ^ 1, 0, kt + 2, cur, 0, kDmaD, full);
+  };
+  // While the stages an iteration loads (kt+1, kt+2) lie wholly inside K,
+  // its DMAs need no mask; the rest take the masked form.
+  const int kfull = kbytes / kFastKBytes;
+  int kt = 0;
+  for (; kt + 2 < kfull; ++kt) iter(kt, std::true_type{});
+  for (; kt < ktiles; ++kt) iter(kt, std::false_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // no LDS write may outlive the loop
   __syncthreads();                                     // and no wave still reads a stage
 
