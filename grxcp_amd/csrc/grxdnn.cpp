@@ -115,6 +115,30 @@ bool row_layout(const grxdnnTensorStruct& t, int64_t* rows, int64_t* pitch) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
+// No two elements of an output share an address: taken in increasing stride
+// order (dimensions of extent 1 aside), each stride covers the extent of the
+// dimensions below it. An input may overlap itself (a broadcast); an output
+// that did would be written by several threads.
+bool no_overlap(const grxdnnTensorStruct& t) {
+  int idx[GRXDNN_DIM_MAX];
+  int n = 0;
+  for (int i = 0; i < t.nb; ++i)
+    if (t.dims[i] > 1) idx[n++] = i;
+  for (int a = 1; a < n; ++a)
+    for (int b = a; b > 0 && t.strides[idx[b]] < t.strides[idx[b - 1]]; --b) {
+      const int x = idx[b];
+      idx[b] = idx[b - 1];
+      idx[b - 1] = x;
+    }
+  int64_t extent = 1;
+  for (int j = 0; j < n; ++j) {
+    const int i = idx[j];
+    if ((int64_t)t.strides[i] < extent) return false;
+    extent = (int64_t)t.strides[i] * t.dims[i];
+  }
+  return true;
+}
+
 grxdnnStatus_t norm_common(grxdnnHandle_t handle, grxdnnTensorDescriptor_t xDesc, const void* x,
                            grxdnnTensorDescriptor_t wDesc, const void* gamma, const void* beta,
                            bool layer, float eps, grxdnnTensorDescriptor_t yDesc, void* y) {
@@ -395,6 +419,7 @@ grxdnnStatus_t grxdnnAttentionForward(grxdnnHandle_t handle, grxdnnAttentionDesc
     for (int i = 0; i < 3; ++i)
       if (d->strides[i] % 8 != 0) return GRXDNN_STATUS_NOT_SUPPORTED;
   }
+  if (!no_overlap(*oDesc)) return GRXDNN_STATUS_INVALID_VALUE;
   if (!q || !k || !v || !o) return GRXDNN_STATUS_INVALID_VALUE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return GRXDNN_STATUS_NOT_SUPPORTED;

@@ -211,6 +211,23 @@ print(a, b if g.device_count() == 0 else 'dev', p.value.decode().endswith('libgr
 
 
 @pytest.mark.skipif(g.device_count() > 0, reason="checks the no-device path")
+def test_attention_broadcast_input_passes_validation():
+    """An input whose rows share addresses (a broadcast) is accepted, and so
+    is an interleaved [B, S, H, D] output: validation passes and the call
+    stops at the missing device."""
+    D = g.load().dnn
+    h = ctypes.c_void_p()
+    assert D.grxdnnCreate(ctypes.byref(h)) == g.SUCCESS
+    ad = g.AttnDesc(True, 0.125)
+    q = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128])
+    shared_rows = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128], [4096, 2048, 0, 1])
+    bshd = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128], [4096, 128, 256, 1])
+    assert D.grxdnnAttentionForward(h, ad.d, shared_rows.d, FAKE, q.d, FAKE, q.d, FAKE, bshd.d,
+                                    FAKE) == g.ARCH_MISMATCH
+    assert D.grxdnnDestroy(h) == g.SUCCESS
+
+
+@pytest.mark.skipif(g.device_count() > 0, reason="checks the no-device path")
 def test_no_device_is_arch_mismatch_not_a_launch():
     L = g.load().blas
     h = ctypes.c_void_p()
@@ -261,6 +278,11 @@ def test_dnn_descriptors_and_validation():
     assert att(h, ad.d, qf32.d, FAKE, qf32.d, FAKE, qf32.d, FAKE, qf32.d, FAKE) == g.NOT_SUPPORTED
     assert att(h, ad.d, q.d, FAKE, q96.d, FAKE, q.d, FAKE, q.d, FAKE) == g.INVALID_VALUE
     assert att(h, ad.d, q.d, None, q.d, FAKE, q.d, FAKE, q.d, FAKE) == g.INVALID_VALUE
+    # an output whose rows share addresses is refused
+    shared_rows = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128], [4096, 2048, 0, 1])
+    assert att(h, ad.d, q.d, FAKE, q.d, FAKE, q.d, FAKE, shared_rows.d, FAKE) == g.INVALID_VALUE
+    heads_over_rows = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128], [4096, 64, 128, 1])
+    assert att(h, ad.d, q.d, FAKE, q.d, FAKE, q.d, FAKE, heads_over_rows.d, FAKE) == g.INVALID_VALUE
     c = ctypes.c_int(); sc = ctypes.c_float()
     assert D.grxdnnGetAttentionDescriptor(ad.d, ctypes.byref(c), ctypes.byref(sc)) == 0
     assert (c.value, sc.value) == (1, 0.125)
