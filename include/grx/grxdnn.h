@@ -126,6 +126,9 @@ grxdnnStatus_t grxdnnGeluForward(grxdnnHandle_t handle, grxdnnGeluMode_t mode,
  * the same length and are aligned at position 0). Q, K, V, O are 4-d
  * [B, H, S, D] descriptors of one type (GRX_R_16BF or GRX_R_16F), innermost
  * stride 1, with equal B, H, S and D. Supported head dimensions: 64, 128.
+ * The other strides are multiples of 8 elements and the pointers 16-byte
+ * aligned (else NOT_SUPPORTED); O's elements must not share addresses (else
+ * INVALID_VALUE), while Q, K and V may (a broadcast).
  * Softmax and both products accumulate in fp32; O is rounded once (RNE). */
 grxdnnStatus_t grxdnnCreateAttentionDescriptor (grxdnnAttentionDescriptor_t* d);
 grxdnnStatus_t grxdnnDestroyAttentionDescriptor(grxdnnAttentionDescriptor_t d);
