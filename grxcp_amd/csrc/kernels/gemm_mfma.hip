@@ -94,7 +94,11 @@ struct KParams {
 // ---------------------------------------------------------------------------
 // epilogue. C is column-major, so a run of consecutive rows i0.. of one column
 // j is contiguous. Each Epi writes one element (put) or a full aligned run of
-// kRun elements, 16 bytes, with one vector access (put_run).
+// kRun elements, 16 bytes, with one vector access (put_run). Runs are stored
+// with the non-temporal (streaming) hint. Every CU finishes its tile at about
+// the same time, so C leaves as a burst of 256 tiles while the matrix cores
+// idle; with the hint the bursts cost less (measured: +4 % on int8 with a
+// 4096x28672 C, +11 % at 16384^2 x 1024, +1-2 % at 8192^3).
 // ---------------------------------------------------------------------------
 
 template <MmaOut OUT>
@@ -123,7 +127,7 @@ struct Epi<MmaOut::F32> {
 #pragma unroll
       for (int q = 0; q < 4; ++q) o[q] = apply(p, v[q], old[q]);
     }
-    *(f32x4*)c = o;
+    __builtin_nontemporal_store(o, (f32x4*)c);
   }
 };
 
@@ -163,7 +167,7 @@ struct EpiNarrow {
         o[h] = pack(apply(p, v[2 * h], (uint16_t)(old[h] & 0xffff)),
                     apply(p, v[2 * h + 1], (uint16_t)(old[h] >> 16)));
     }
-    *(u32x4*)c = o;
+    __builtin_nontemporal_store(o, (u32x4*)c);
   }
 };
 template <> struct Epi<MmaOut::BF16> : EpiNarrow<MmaOut::BF16> {};
@@ -187,7 +191,7 @@ struct Epi<MmaOut::I32> {
     i32x4 o;
 #pragma unroll
     for (int q = 0; q < 4; ++q) o[q] = apply(p, v[q], old[q]);
-    *(i32x4*)c = o;
+    __builtin_nontemporal_store(o, (i32x4*)c);
   }
 };
 
@@ -207,7 +211,7 @@ struct Epi<MmaOut::DEQ_BF16> {
 #pragma unroll
     for (int h = 0; h < 4; ++h)
       o[h] = pack_bf16x2(__fmul_rn((float)v[2 * h], s), __fmul_rn((float)v[2 * h + 1], s));
-    *(u32x4*)c = o;
+    __builtin_nontemporal_store(o, (u32x4*)c);
   }
 };
 
