@@ -159,7 +159,10 @@ void sgemm_mfma(SParams p) {
   }
 
   // C = alpha*acc + beta*C (col-major); lane holds column l32 of each MFMA
-  // tile and rows 8*(r/4) + 4*hh + r%4.
+  // tile and rows 8*(r/4) + 4*hh + r%4: runs of 4 rows, one 16-byte
+  // non-temporal store each where the run lies inside C and C's columns are
+  // 16-byte aligned, element by element otherwise (same arithmetic).
+  const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)C & 15) == 0;
 #pragma unroll
   for (int fm = 0; fm < NF; ++fm)
 #pragma unroll
@@ -167,12 +170,28 @@ void sgemm_mfma(SParams p) {
       const int gj = col0 + WT * wn + 32 * fn + l32;
       if (gj >= p.n) continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gi = row0 + WT * wm + 32 * fm + 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (gi >= p.m) continue;
-        float* cp = C + (int64_t)gj * p.ldc + gi;
-        const float v = __fmul_rn(p.alpha, acc[fm][fn][r]);
-        *cp = (p.beta == 0.0f) ? v : __fadd_rn(v, __fmul_rn(p.beta, *cp));
+      for (int g = 0; g < 4; ++g) {
+        const int i0 = row0 + WT * wm + 32 * fm + 8 * g + 4 * hh;
+        if (i0 >= p.m) continue;
+        float* cp = C + (int64_t)gj * p.ldc + i0;
+        if (vec && i0 + 4 <= p.m) {
+          f32x4 o;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[q] = __fmul_rn(p.alpha, acc[fm][fn][4 * g + q]);
+          if (p.beta != 0.0f) {
+            const f32x4 old = *(const f32x4*)cp;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = __fadd_rn(o[q], __fmul_rn(p.beta, old[q]));
+          }
+          __builtin_nontemporal_store(o, (f32x4*)cp);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (i0 + q >= p.m) break;
+            const float v = __fmul_rn(p.alpha, acc[fm][fn][4 * g + q]);
+            cp[q] = (p.beta == 0.0f) ? v : __fadd_rn(v, __fmul_rn(p.beta, cp[q]));
+          }
+        }
       }
     }
   cycle_record(p.probe, t0, (uint32_t)((bz * gridDim.x + blockIdx.x) * 4 + wave), wave);
