@@ -71,6 +71,13 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :: "s"(lds), "v"(voff), "s"(rsrc) : "memory");
 }
+// The same with a wave-uniform byte offset in the instruction's soffset. The
+// buffer's range check sees only the per-lane offset, so this form is for
+// rows known to lie inside the tensor.
+__device__ __forceinline__ void dma16_so(i32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory");
+}
 
 template <AttnType T> struct AIo;
 template <> struct AIo<AttnType::BF16> {
@@ -204,19 +211,40 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
 
   // DMA: instruction i of wave w fills rows RPI*(IPW*w + i) .. of K or V;
   // lane L lands in row +L/CH at physical chunk L%CH.
+  // The tile-invariant part of each DMA's offset (row within the tile and
+  // swizzled chunk). A tile whose rows all lie inside the sequence takes it
+  // with the tile's offset in soffset: no VALU work per DMA. The last,
+  // ragged tile and the prefetch past the end keep the masked form, whose
+  // per-lane offsets the buffer's range check turns into zeros.
+  uint32_t kbase[IPW], vbase[IPW];
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int blk = IPW * wave + i;
+    const int row = RPI * blk + lane / CH;
+    const int pc = lane % CH;
+    kbase[i] = (uint32_t)row * k_rs + (uint32_t)(16 * (pc ^ kswz<D>(row)));
+    vbase[i] = (uint32_t)row * v_rs + (uint32_t)(16 * (pc ^ vswz<D>(row)));
+  }
   auto dma_tile = [&](int t, int st) {
     const int kv0 = t * kBK;
+    if (kv0 + kBK <= p.S) {
+      const uint32_t ks = (uint32_t)kv0 * k_rs, vs = (uint32_t)kv0 * v_rs;
 #pragma unroll
-    for (int i = 0; i < IPW; ++i) {
-      const int blk = IPW * wave + i;
-      const int row = RPI * blk + lane / CH;
-      const int pc = lane % CH;
-      const bool ok = t < ntiles;
-      const uint32_t kr = (uint32_t)(kv0 + row);
-      const uint32_t ko = ok ? kr * k_rs + (uint32_t)(16 * (pc ^ kswz<D>(row))) : 0x80000000u;
-      const uint32_t vo = ok ? kr * v_rs + (uint32_t)(16 * (pc ^ vswz<D>(row))) : 0x80000000u;
-      dma16(rk, lds_addr(&lds[st][0][blk * 64]), ko);
-      dma16(rv, lds_addr(&lds[st][1][blk * 64]), vo);
+      for (int i = 0; i < IPW; ++i) {
+        const int blk = IPW * wave + i;
+        dma16_so(rk, lds_addr(&lds[st][0][blk * 64]), kbase[i], ks);
+        dma16_so(rv, lds_addr(&lds[st][1][blk * 64]), vbase[i], vs);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < IPW; ++i) {
+        const int blk = IPW * wave + i;
+        const bool ok = t < ntiles;
+        const uint32_t ko = ok ? (uint32_t)kv0 * k_rs + kbase[i] : 0x80000000u;
+        const uint32_t vo = ok ? (uint32_t)kv0 * v_rs + vbase[i] : 0x80000000u;
+        dma16(rk, lds_addr(&lds[st][0][blk * 64]), ko);
+        dma16(rv, lds_addr(&lds[st][1][blk * 64]), vo);
+      }
     }
   };
 
