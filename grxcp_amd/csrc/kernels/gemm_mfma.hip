@@ -98,8 +98,17 @@ struct KParams {
 // with the non-temporal (streaming) hint. Every CU finishes its tile at about
 // the same time, so C leaves as a burst of 256 tiles while the matrix cores
 // idle; with the hint the bursts cost less (measured: +4 % on int8 with a
-// 4096x28672 C, +11 % at 16384^2 x 1024, +1-2 % at 8192^3).
+// 4096x28672 C, +11 % at 16384^2 x 1024, +1-2 % at 8192^3). Split-K
+// partials, which the reduction reads back at once, take plain stores.
 // ---------------------------------------------------------------------------
+
+// One 16-byte run of C: streamed (non-temporal) unless STREAM is false, for
+// an output that is read back right away (split-K partials).
+template <bool STREAM, class V>
+__device__ __forceinline__ void put16(void* c, V o) {
+  if constexpr (STREAM) __builtin_nontemporal_store(o, (V*)c);
+  else *(V*)c = o;
+}
 
 template <MmaOut OUT>
 struct Epi;
@@ -117,6 +126,7 @@ struct Epi<MmaOut::F32> {
   __device__ static void put(const KParams& p, T* c, float v, int) {
     *c = apply(p, v, p.beta != 0.0f ? *c : 0.0f);
   }
+  template <bool STREAM = true>
   __device__ static void put_run(const KParams& p, T* c, const float* v, int) {
     f32x4 o;
     if (p.beta == 0.0f) {
@@ -127,7 +137,7 @@ struct Epi<MmaOut::F32> {
 #pragma unroll
       for (int q = 0; q < 4; ++q) o[q] = apply(p, v[q], old[q]);
     }
-    __builtin_nontemporal_store(o, (f32x4*)c);
+    put16<STREAM>(c, o);
   }
 };
 
@@ -154,6 +164,7 @@ struct EpiNarrow {
     if constexpr (OUT == MmaOut::BF16) return pack_bf16x2(a, b);
     else return pack_f16x2(a, b);
   }
+  template <bool STREAM = true>
   __device__ static void put_run(const KParams& p, T* c, const float* v, int) {
     u32x4 o;
     if (p.beta == 0.0f) {
@@ -167,7 +178,7 @@ struct EpiNarrow {
         o[h] = pack(apply(p, v[2 * h], (uint16_t)(old[h] & 0xffff)),
                     apply(p, v[2 * h + 1], (uint16_t)(old[h] >> 16)));
     }
-    __builtin_nontemporal_store(o, (u32x4*)c);
+    put16<STREAM>(c, o);
   }
 };
 template <> struct Epi<MmaOut::BF16> : EpiNarrow<MmaOut::BF16> {};
@@ -185,13 +196,14 @@ struct Epi<MmaOut::I32> {
   __device__ static void put(const KParams& p, T* c, int v, int) {
     *c = apply(p, v, p.ibeta != 0 ? *c : 0);
   }
+  template <bool STREAM = true>
   __device__ static void put_run(const KParams& p, T* c, const int* v, int) {
     i32x4 old = {0, 0, 0, 0};
     if (p.ibeta != 0) old = *(const i32x4*)c;
     i32x4 o;
 #pragma unroll
     for (int q = 0; q < 4; ++q) o[q] = apply(p, v[q], old[q]);
-    __builtin_nontemporal_store(o, (i32x4*)c);
+    put16<STREAM>(c, o);
   }
 };
 
@@ -205,25 +217,26 @@ struct Epi<MmaOut::DEQ_BF16> {
     return f32_to_bf16(__fmul_rn((float)acc, s));
   }
   __device__ static void put(const KParams& p, T* c, int v, int j) { *c = apply(p.scale[j], v); }
+  template <bool STREAM = true>
   __device__ static void put_run(const KParams& p, T* c, const int* v, int j) {
     const float s = p.scale[j];
     u32x4 o;
 #pragma unroll
     for (int h = 0; h < 4; ++h)
       o[h] = pack_bf16x2(__fmul_rn((float)v[2 * h], s), __fmul_rn((float)v[2 * h + 1], s));
-    __builtin_nontemporal_store(o, (u32x4*)c);
+    put16<STREAM>(c, o);
   }
 };
 
 // `count` consecutive rows i0.. of column j (j < n). With `vec`, the caller
 // guarantees a run of kRun elements starting at i0 is 16-byte aligned.
-template <MmaOut OUT, class E>
+template <MmaOut OUT, bool STREAM = true, class E>
 __device__ __forceinline__ void store_run(const KParams& p, int i0, int j, const E* v, int count,
                                           bool vec) {
   using P = Epi<OUT>;
   typename P::T* c = (typename P::T*)p.c + (int64_t)j * p.ldc + i0;
   if (vec && count == P::kRun && i0 + P::kRun <= p.m) {
-    P::put_run(p, c, v, j);
+    P::template put_run<STREAM>(p, c, v, j);
   } else {
     for (int q = 0; q < count; ++q)
       if (i0 + q < p.m) P::put(p, c + q, v[q], j);
@@ -307,7 +320,7 @@ __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <class Op, MmaOut OUT>
+template <class Op, MmaOut OUT, bool STREAM = true>
 __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
   const KParams p = batch_view(batch_p);
   // [stage][A | B][row * 8 + physical chunk], 16 bytes per entry: 128 KB.
@@ -535,7 +548,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
         const int col = rd * kColsPerRound + rcol;
         E v[kRun];
         read_run(col, v);
-        Epi<OUT>::put_run(p, cbase + (int64_t)col * p.ldc, v, gj0 + col);
+        Epi<OUT>::template put_run<STREAM>(p, cbase + (int64_t)col * p.ldc, v, gj0 + col);
       }
     } else {
       for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
@@ -543,7 +556,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
         E v[kRun];
         read_run(col, v);
         const int gj = gj0 + col;
-        if (gj < p.n && gi < p.m) store_run<OUT>(p, gi, gj, v, kRun, true);
+        if (gj < p.n && gi < p.m) store_run<OUT, STREAM>(p, gi, gj, v, kRun, true);
       }
     }
     asm volatile("" ::: "memory");
@@ -979,7 +992,7 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     q.probe = nullptr;
     q.tiles_m = (g->m + kFastTile - 1) / kFastTile;
     q.tiles_n = (g->n + kFastTile - 1) / kFastTile;
-    hipLaunchKernelGGL((gemm_tn_fast<Op, RAW>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256), 0,
+    hipLaunchKernelGGL((gemm_tn_fast<Op, RAW, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256), 0,
                        s, q);
     constexpr int R = Epi<OUT>::kRun;
     const int64_t items = (int64_t)((g->m + R - 1) / R) * g->n;
