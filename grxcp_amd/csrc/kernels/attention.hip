@@ -25,7 +25,7 @@
 //    divided by the row sum once at the end and rounded once;
 //  * registers: this file is compiled with MFMA results in VGPRs
 //    (-amdgpu-mfma-vgpr-form), which keeps the scores, P and O out of
-//    AGPR<->VGPR copies (184 VGPRs, two waves per SIMD);
+//    AGPR<->VGPR copies (194 VGPRs, two waves per SIMD);
 //  * causal: key tiles past the query tile are never loaded; a 32-query block
 //    skips tiles entirely above its diagonal; workgroups run heaviest first,
 //    and all query tiles of a head run on one XCD (K/V shared in its L2).
