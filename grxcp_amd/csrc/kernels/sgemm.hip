@@ -48,9 +48,12 @@ struct SParams {
 // contiguous dimension are one aligned 16-byte load; a stage wholly inside
 // the matrices (decided once per stage, uniformly) takes those loads with no
 // per-element guard, other stages the guarded path. (Measured at 4096^3:
-// 91 -> 129 TFLOP/s against one kernel with run-time transposes and guards.
-// A pitch that puts k-rows 2s and 2s+1 half the banks apart measured 3 %
-// slower: its LDS footprint leaves 3 instead of 4 workgroups per CU.)
+// 91 -> 129 TFLOP/s against one kernel with run-time transposes and guards,
+// 129 -> 134 with the fragment reads one k-step ahead. Slower, same output:
+// a pitch that puts k-rows 2s and 2s+1 half the banks apart (3 %: 3 instead
+// of 4 workgroups per CU), an XOR-swizzled unpadded layout (4 %), 32-deep
+// stages (2 workgroups per CU, 5-9 %), 256x256 tiles (one wave per SIMD,
+// 4 %), the next stage's LDS stores moved to mid-stage (no change).)
 template <int MT, bool VEC, bool TA, bool TB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
 void sgemm_mfma(SParams p) {
@@ -139,19 +142,32 @@ void sgemm_mfma(SParams p) {
   for (int k0 = 0; k0 < p.k; k0 += kK) {
     const bool more = k0 + kK < p.k;
     if (more) load(k0 + kK);
+    // Fragments one k-step ahead: step s+1's LDS reads are issued before
+    // step s's MFMAs (the scheduling barriers keep that order), so each
+    // wait covers reads issued a whole step earlier.
+    float av[2][NF], bv[2][NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      av[0][f] = As[buf][hh][WT * wm + 32 * f + l32];
+      bv[0][f] = Bs[buf][hh][WT * wn + 32 * f + l32];
+    }
 #pragma unroll
     for (int s = 0; s < kK / 2; ++s) {
-      float av[NF], bv[NF];
+      if (s + 1 < kK / 2) {
 #pragma unroll
-      for (int f = 0; f < NF; ++f) {
-        av[f] = As[buf][2 * s + hh][WT * wm + 32 * f + l32];
-        bv[f] = Bs[buf][2 * s + hh][WT * wn + 32 * f + l32];
+        for (int f = 0; f < NF; ++f) {
+          av[(s + 1) & 1][f] = As[buf][2 * s + 2 + hh][WT * wm + 32 * f + l32];
+          bv[(s + 1) & 1][f] = Bs[buf][2 * s + 2 + hh][WT * wn + 32 * f + l32];
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int fm = 0; fm < NF; ++fm)
 #pragma unroll
         for (int fn = 0; fn < NF; ++fn)
-          acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[fm], bv[fn], acc[fm][fn], 0, 0, 0);
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s & 1][fm], bv[s & 1][fn], acc[fm][fn],
+                                                             0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (more) store(buf ^ 1);
     __syncthreads();
