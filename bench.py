@@ -213,7 +213,9 @@ def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu):
 
 
 def bench_sgemm(stream, blas, steps, warmup):
-    """grxblasSgemm fp32 4096^3 (N, N, column-major), fp32 matrix-core roofline."""
+    """grxblasSgemm fp32 4096^3 (N, N, column-major), fp32 matrix-core roofline.
+    The call copies A K-contiguous (transpose_k) and runs the 256x256-tile
+    kernel; the timed region holds both."""
     M = N = K = 4096
     log("Sgemm 4096^3: generating inputs")
     A = synth.uniform_f32(M * K, 41, -1.0, 1.0)

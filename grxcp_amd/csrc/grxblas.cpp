@@ -563,6 +563,27 @@ static grxblasStatus_t sgemm_batched(grxblasHandle_t handle, grxblasOperation_t 
   d.c = (float*)C; d.ldc = ldc; d.stride_c = strideC;
   d.alpha = *alpha; d.beta = *beta;
   d.probe = probe;
+  if (!probe) {
+    // Problems that fill the GPU with 256x256 tiles run the GemmEx TN kernel
+    // on fp32 (behind K-contiguous copies for other layouts) when its
+    // workspace is there; the rest, and calls with a cycle probe, sgemm_mfma.
+    grxk::GemmDesc g{};
+    g.m = m; g.n = n; g.k = k; g.batch = batch;
+    g.ta = d.ta; g.tb = d.tb;
+    g.a = A; g.lda = lda; g.stride_a = strideA;
+    g.b = B; g.ldb = ldb; g.stride_b = strideB;
+    g.c = C; g.ldc = ldc; g.stride_c = strideC;
+    g.alpha = *alpha; g.beta = *beta;
+    if (grxk::fp32_mma_wanted(g)) {
+      std::lock_guard<std::mutex> lock(handle->mutex);
+      hipError_t e = attach_workspace_locked(*handle, grxk::MmaIn::F32, grxk::MmaOut::F32, g,
+                                             handle->stream);
+      if (e == hipSuccess &&
+          grxk::gemm_workspace_bytes(grxk::MmaIn::F32, grxk::MmaOut::F32, g) <= g.ws_bytes)
+        return from_hip(grxk::launch_mma_gemm(grxk::MmaIn::F32, grxk::MmaOut::F32, g,
+                                              handle->stream));
+    }
+  }
   return from_hip(grxk::launch_sgemm(d, handle->stream));
 }
 

@@ -75,6 +75,23 @@ struct OpI8 {
   }
 };
 
+// fp32 (Sgemm): a 16-byte fragment is 4 floats, k = 4*(lane/32) + s of an
+// 8-float slice of K; v_mfma_f32_32x32x2_f32 step s pairs k = s (lanes 0-31)
+// with k = 4 + s (lanes 32-63), so 4 steps cover the slice.
+struct OpF32 {
+  static constexpr const char* kName = "f32";
+  using Acc = f32x16;
+  using Elem = float;
+  static constexpr int kElemBytes = 4;
+  __device__ static Acc mma(i32x4 a, i32x4 b, Acc c) {
+    // Whole-vector casts: a bit cast of one element (a[s]) reads element 0.
+    const f32x4 af = __builtin_bit_cast(f32x4, a), bf = __builtin_bit_cast(f32x4, b);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s], bf[s], c, 0, 0, 0);
+    return c;
+  }
+};
+
 struct KParams {
   const uint8_t* a;
   const uint8_t* b;
@@ -621,6 +638,7 @@ template <class Op, MmaOut OUT>
 __global__ __launch_bounds__(256) void gemm_general(KParams batch_p) {
   const KParams p = batch_view(batch_p);
   constexpr int EB = Op::kElemBytes;
+  using U = std::conditional_t<EB == 4, uint32_t, std::conditional_t<EB == 2, uint16_t, uint8_t>>;
   constexpr int KT = kGenKBytes / EB;  // elements of K per stage
   __shared__ __attribute__((aligned(16))) uint8_t sa[kGenTile * kGenRowBytes];
   __shared__ __attribute__((aligned(16))) uint8_t sb[kGenTile * kGenRowBytes];
@@ -657,11 +675,9 @@ __global__ __launch_bounds__(256) void gemm_general(KParams batch_p) {
       uint8_t* dst = sa + r * kGenRowBytes + kk * EB;
       if (gi < p.m && gk < p.k) {
         const int64_t off = p.ta ? ((int64_t)gi * p.lda + gk) : ((int64_t)gk * p.lda + gi);
-        if constexpr (EB == 2) *(uint16_t*)dst = ((const uint16_t*)p.a)[off];
-        else *dst = p.a[off];
+        *(U*)dst = ((const U*)p.a)[off];
       } else {
-        if constexpr (EB == 2) *(uint16_t*)dst = 0;
-        else *dst = 0;
+        *(U*)dst = 0;
       }
     }
 #pragma unroll
@@ -673,11 +689,9 @@ __global__ __launch_bounds__(256) void gemm_general(KParams batch_p) {
       uint8_t* dst = sb + c * kGenRowBytes + kk * EB;
       if (gj < p.n && gk < p.k) {
         const int64_t off = p.tb ? ((int64_t)gk * p.ldb + gj) : ((int64_t)gj * p.ldb + gk);
-        if constexpr (EB == 2) *(uint16_t*)dst = ((const uint16_t*)p.b)[off];
-        else *dst = p.b[off];
+        *(U*)dst = ((const U*)p.b)[off];
       } else {
-        if constexpr (EB == 2) *(uint16_t*)dst = 0;
-        else *dst = 0;
+        *(U*)dst = 0;
       }
     }
     __syncthreads();
@@ -735,7 +749,10 @@ __global__ __launch_bounds__(256) void transpose_k(const uint8_t* X, int64_t ldx
     const int gr = r0 + r, gc = c0 + ch * VE;
     if (gr >= R || gc >= C) continue;
     u32x4 w;
-    if constexpr (EB == 2) {
+    if constexpr (EB == 4) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) w[h] = *(const uint32_t*)&tile[ch * VE + h][4 * r];
+    } else if constexpr (EB == 2) {
 #pragma unroll
       for (int h = 0; h < 4; ++h)
         w[h] = (uint32_t)*(const uint16_t*)&tile[ch * VE + 2 * h][2 * r] |
@@ -829,7 +846,7 @@ constexpr int out_bytes() { return (OUT == MmaOut::F32 || OUT == MmaOut::I32) ? 
 // The TN kernel's requirements: K-contiguous operands whose rows start on
 // 16-byte boundaries (so every staged chunk is one aligned 16-byte load),
 // 32-bit buffer offsets within a 256-row panel, and a C whose columns start
-// on 16-byte boundaries (ldc % 8 == 0, aligned C), so that a run of 4 (32-bit)
+// on 16-byte boundaries (ldc * sizeof(C) % 16 == 0, aligned C), so that a run of 4 (32-bit)
 // or 8 (16-bit) rows of one column is one vector store.
 template <class Op, MmaOut OUT>
 bool tn_ready(const GemmDesc& d) {
@@ -838,7 +855,7 @@ bool tn_ready(const GemmDesc& d) {
   return d.ta && !d.tb && d.k > 0 && ((int64_t)d.k * EB) % 16 == 0 &&
          (d.lda * EB) % 16 == 0 && (d.ldb * EB) % 16 == 0 &&
          ((uintptr_t)d.a % 16) == 0 && ((uintptr_t)d.b % 16) == 0 &&
-         d.ldc % 8 == 0 && ((uintptr_t)d.c % 16) == 0 &&
+         (d.ldc * OB) % 16 == 0 && ((uintptr_t)d.c % 16) == 0 &&
          (d.stride_a * EB) % 16 == 0 && (d.stride_b * EB) % 16 == 0 &&
          (d.stride_c * OB) % 16 == 0 &&
          (int64_t)kFastTile * d.lda * EB < (1ll << 31) &&
@@ -909,7 +926,8 @@ Plan make_plan(const GemmDesc& d) {
       t = c;
     }
   }
-  if (!t.tn || d.batch != 1 || d.probe) return t;
+  // fp32 stages take 8x the MFMA time of 16-bit ones: the split model does not apply.
+  if (!t.tn || d.batch != 1 || d.probe || std::is_same<Op, OpF32>::value) return t;
   // Split K where a cost model (times in ns, fitted to kernel traces of
   // 256x256 tiles at up to 256 workgroups) predicts at least 10 % less time.
   // One pass: kFixNs (launch, prologue, epilogue) + kStageNs per 128-byte K
@@ -1080,6 +1098,9 @@ hipError_t launch_mma_gemm(MmaIn in, MmaOut out, const GemmDesc& d, hipStream_t 
       if (out == MmaOut::I32) return run<OpI8, MmaOut::I32>(d, s);
       if (out == MmaOut::DEQ_BF16) return run<OpI8, MmaOut::DEQ_BF16>(d, s);
       break;
+    case MmaIn::F32:
+      if (out == MmaOut::F32) return run<OpF32, MmaOut::F32>(d, s);
+      break;
   }
   return hipErrorNotSupported;
 }
@@ -1098,8 +1119,25 @@ size_t gemm_workspace_bytes(MmaIn in, MmaOut out, const GemmDesc& d) {
       if (out == MmaOut::I32) return workspace<OpI8, MmaOut::I32>(d);
       if (out == MmaOut::DEQ_BF16) return workspace<OpI8, MmaOut::DEQ_BF16>(d);
       break;
+    case MmaIn::F32:
+      if (out == MmaOut::F32) return workspace<OpF32, MmaOut::F32>(d);
+      break;
   }
   return 0;
+}
+
+// One workgroup per CU, so tiles run in waves of 256; a last wave that is
+// mostly empty costs a whole wave here, where sgemm_mfma (4 workgroups of
+// 128x128 per CU) finishes such a tail sooner (4000x4100x1000: 68 against
+// 87 TFLOP/s). Taken with at least 4 waves, or a last wave at least 3/4 full.
+bool fp32_mma_wanted(const GemmDesc& d) {
+  if (d.probe || d.m <= 0 || d.n <= 0 || d.batch <= 0) return false;
+  const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
+  const int64_t units = tiles * d.batch;
+  const int64_t waves = (units + 255) / 256;
+  const int64_t last = units - (waves - 1) * 256;
+  if (units < 256 || (waves < 4 && last < 192)) return false;
+  return make_plan<OpF32, MmaOut::F32>(d).tn;
 }
 
 }  // namespace grxk

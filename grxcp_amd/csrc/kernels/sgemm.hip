@@ -10,7 +10,9 @@
 // shapes, any leading dimension). The batch is the grid's z dimension with
 // signed element strides (a zero stride broadcasts an operand), exactly the
 // reference's one-launch batching (ref: src/libs/grxblas/grxblas.cpp:936-938).
-// beta == 0 never reads C (ref: kernels/sgemm.cpp:80-85).
+// beta == 0 never reads C (ref: kernels/sgemm.cpp:80-85). Problems that
+// fill the GPU with 256x256 tiles run gemm_mfma.hip's TN kernel on fp32
+// instead (grxblas.cpp sgemm_batched).
 //
 // Level 1/2 follow the reference's semantics (ref: kernels/blas12.cpp:41-132):
 // BLAS increments (negative walks backwards), sgemv beta == 0 never reads y.

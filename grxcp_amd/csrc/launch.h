@@ -12,7 +12,7 @@
 namespace grxk {
 
 // Element types the matrix-core GEMM reads and the epilogue it ends in.
-enum class MmaIn { BF16, F16, I8 };
+enum class MmaIn { BF16, F16, I8, F32 };   // F32: Sgemm's large problems
 enum class MmaOut {
   F32,        // alpha*acc + beta*C, fp32 C
   BF16,       // same, rounded to bf16 (RNE)
@@ -43,6 +43,9 @@ hipError_t launch_mma_gemm(MmaIn in, MmaOut out, const GemmDesc& d, hipStream_t 
 // Workspace bytes launch_mma_gemm would use for d (0: it needs none). With a
 // smaller d.ws_bytes the call takes the general path instead.
 size_t gemm_workspace_bytes(MmaIn in, MmaOut out, const GemmDesc& d);
+// fp32 problem d (MmaIn::F32 -> MmaOut::F32, no probe) that fills the GPU
+// with 256x256 tiles and can run the TN kernel, directly or behind copies.
+bool fp32_mma_wanted(const GemmDesc& d);
 // Upper bound of probe slots any GEMM launch for an m x n output uses.
 int64_t gemm_probe_slots(int m, int n);
 

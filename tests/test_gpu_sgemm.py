@@ -89,6 +89,24 @@ def test_reference_batched_gate(blas):
     assert run_batched(blas, 0, 0, 7, 3, 5, 1.0, 0.0, 1, 4, False) == 0
 
 
+def test_large_sgemm_runs_the_256_tile_kernel(blas, capfd):
+    """Problems that fill the GPU with 256x256 tiles run the GemmEx TN kernel
+    on fp32 (the other layouts behind K-contiguous copies): a batch of 64
+    512x512 products in every layout, gaps between batch members and a
+    broadcast B, and a ragged batched shape; the batched gate's tolerance over
+    the whole buffer, gaps included. The library's GRXBLAS_LOG line names the
+    kernel each call ran."""
+    from test_gpu_gemm import logged_plans
+    cases = [(ta, tb, 512, 512, 132, 1.5, -0.5, 64, 4, tb == 1) for ta in (0, 1) for tb in (0, 1)]
+    cases += [(0, 0, 300, 500, 240, 1.0, 0.0, 64, 0, False), (1, 0, 300, 500, 240, 1.0, 1.0, 64, 8, True)]
+    for c in cases:
+        res = []
+        plans = logged_plans(capfd, lambda: res.append(run_batched(blas, *c)))
+        assert res == [0], (c, res)
+        assert len(plans) == 1 and plans[0]["kernel"] == "tn256", (c, plans)
+        assert plans[0]["copy_a"] == str(int(not c[0])) and plans[0]["copy_b"] == str(int(c[1])), (c, plans)
+
+
 def test_config1_sgemm_512_cubed(blas):
     """fp32 C = A*B, 512^3 row-major, alpha=1 beta=0, U[-1,1]
     from seeds 1 and 2, mapped to column-major as C^T = B^T A^T:
