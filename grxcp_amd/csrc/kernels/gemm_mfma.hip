@@ -20,9 +20,11 @@
 //    32x32 MFMA tile each. This is the path the reference's ragged and
 //    transposed gate cases exercise.
 //
-// Both kernels are byte-generic: every v_mfma used consumes 16 bytes of A and
-// 16 bytes of B per lane (8 bf16/fp16 or 16 int8) and produces the same 32x32
-// accumulator layout, so one body serves all three input types.
+// Both kernels are byte-generic: every matrix-core step consumes 16 bytes of
+// A and 16 bytes of B per lane (8 bf16/fp16 or 16 int8 in one v_mfma, 4 fp32
+// in four v_mfma_f32_32x32x2_f32) and produces the same 32x32 accumulator
+// layout, so one body serves all four input types. fp32 serves Sgemm's
+// problems that fill the GPU (grxblas.cpp sgemm_batched).
 //
 // Accumulator layout of a 32x32 MFMA (verified on gfx950 by
 // tests/test_gpu_gemm.py): lane l, element r holds row
