@@ -875,6 +875,9 @@ bool tn_ready(const GemmDesc& d) {
 constexpr int kSplitTiles = 256;
 constexpr int kMaxSplit = 16;
 constexpr int64_t kFixNs = 8000, kStageNs = 1030, kReduceNs = 6000, kPartialBytesPerNs = 10000;
+// An fp32 stage (32 elements of K) is 8x the MFMA work of a 16-bit one; measured
+// 905 us for 128 stages per workgroup at 4096^3 (the chip holds ~2.4 GHz there).
+constexpr int64_t kStageNsF32 = 7070;
 
 struct Plan {
   bool copy_a = false, copy_b = false;
@@ -928,8 +931,7 @@ Plan make_plan(const GemmDesc& d) {
       t = c;
     }
   }
-  // fp32 stages take 8x the MFMA time of 16-bit ones: the split model does not apply.
-  if (!t.tn || d.batch != 1 || d.probe || std::is_same<Op, OpF32>::value) return t;
+  if (!t.tn || d.batch != 1 || d.probe) return t;
   // Split K where a cost model (times in ns, fitted to kernel traces of
   // 256x256 tiles at up to 256 workgroups) predicts at least 10 % less time.
   // One pass: kFixNs (launch, prologue, epilogue) + kStageNs per 128-byte K
@@ -944,8 +946,9 @@ Plan make_plan(const GemmDesc& d) {
   const int64_t stages = ((int64_t)d.k * EB + kFastKBytes - 1) / kFastKBytes;
   if (tiles >= kSplitTiles || stages < 16) return t;
   const int64_t mn = ((int64_t)d.m + 7) / 8 * 8 * d.n;
+  constexpr int64_t kStage = std::is_same<Op, OpF32>::value ? kStageNsF32 : kStageNs;
   auto cost = [&](int64_t sl, int64_t per) {
-    return kFixNs + kStageNs * per + (sl > 1 ? kReduceNs + 8 * sl * mn / kPartialBytesPerNs : 0);
+    return kFixNs + kStage * per + (sl > 1 ? kReduceNs + 8 * sl * mn / kPartialBytesPerNs : 0);
   };
   const int64_t one = cost(1, stages);
   int split = 1, per_best = (int)stages;
@@ -1128,18 +1131,20 @@ size_t gemm_workspace_bytes(MmaIn in, MmaOut out, const GemmDesc& d) {
   return 0;
 }
 
-// One workgroup per CU, so tiles run in waves of 256; a last wave that is
-// mostly empty costs a whole wave here, where sgemm_mfma (4 workgroups of
-// 128x128 per CU) finishes such a tail sooner (4000x4100x1000: 68 against
-// 87 TFLOP/s). Taken with at least 4 waves, or a last wave at least 3/4 full.
+// One workgroup per CU, so workgroups (tiles x batch x K slices) run in
+// waves of 256; a last wave that is mostly empty costs a whole wave here,
+// where sgemm_mfma (4 workgroups of 128x128 per CU) finishes such a tail
+// sooner (4000x4100x1000: 68 against 87 TFLOP/s). Taken with at least 4
+// waves, or a last wave at least 3/4 full.
 bool fp32_mma_wanted(const GemmDesc& d) {
   if (d.probe || d.m <= 0 || d.n <= 0 || d.batch <= 0) return false;
+  const Plan t = make_plan<OpF32, MmaOut::F32>(d);
+  if (!t.tn) return false;
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
-  const int64_t units = tiles * d.batch;
+  const int64_t units = tiles * d.batch * t.split;
   const int64_t waves = (units + 255) / 256;
   const int64_t last = units - (waves - 1) * 256;
-  if (units < 256 || (waves < 4 && last < 192)) return false;
-  return make_plan<OpF32, MmaOut::F32>(d).tn;
+  return units >= 256 && (waves >= 4 || last >= 192);
 }
 
 }  // namespace grxk

@@ -107,6 +107,19 @@ def test_large_sgemm_runs_the_256_tile_kernel(blas, capfd):
         assert plans[0]["copy_a"] == str(int(not c[0])) and plans[0]["copy_b"] == str(int(c[1])), (c, plans)
 
 
+def test_sgemm_split_k_on_the_256_tile_kernel(blas, capfd):
+    """Too few 256x256 tiles for the GPU but long enough in K: the fp32 problem
+    is split along K (64 tiles x 4 slices) on the same kernel, after the
+    operand copy for (N, N); the reference gate's tolerance in the m x n
+    window and bit-exact padding, against the oracle."""
+    from test_gpu_gemm import logged_plans
+    for ta in (1, 0):
+        res = []
+        plans = logged_plans(capfd, lambda: res.append(run_case(blas, ta, 0, 2048, 2048, 1024, 1.0, 0.5)))
+        assert res == [(0, 0)], (ta, res)
+        assert len(plans) == 1 and plans[0]["kernel"] == "tn256" and int(plans[0]["split"]) == 4, plans
+
+
 def test_config1_sgemm_512_cubed(blas):
     """fp32 C = A*B, 512^3 row-major, alpha=1 beta=0, U[-1,1]
     from seeds 1 and 2, mapped to column-major as C^T = B^T A^T:
