@@ -942,18 +942,26 @@ Plan make_plan(const GemmDesc& d) {
   // partials written by the slices and read back, 8 * s * m * n bytes at
   // kPartialBytesPerNs (mostly served from the last-level cache, hence above
   // the HBM rate).
+  // fp32 stages are long enough (8x the MFMA work) that slices may also run
+  // in several waves of 256 workgroups: there the model charges ceil(tiles *
+  // s / 256) waves of ceil(stages/s) stages (3072^3: 144 tiles in 7 slices,
+  // 4 waves; 99 -> 109 TFLOP/s against the 128x128 kernel). Problems of 256
+  // tiles or more are not split (their alternative is that kernel, which
+  // finishes a partial last wave sooner than this model assumes).
+  constexpr bool kF32 = std::is_same<Op, OpF32>::value;
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
   const int64_t stages = ((int64_t)d.k * EB + kFastKBytes - 1) / kFastKBytes;
   if (tiles >= kSplitTiles || stages < 16) return t;
   const int64_t mn = ((int64_t)d.m + 7) / 8 * 8 * d.n;
-  constexpr int64_t kStage = std::is_same<Op, OpF32>::value ? kStageNsF32 : kStageNs;
+  constexpr int64_t kStage = kF32 ? kStageNsF32 : kStageNs;
   auto cost = [&](int64_t sl, int64_t per) {
-    return kFixNs + kStage * per + (sl > 1 ? kReduceNs + 8 * sl * mn / kPartialBytesPerNs : 0);
+    const int64_t waves = kF32 ? (tiles * sl + 255) / 256 : 1;
+    return kFixNs + kStage * per * waves + (sl > 1 ? kReduceNs + 8 * sl * mn / kPartialBytesPerNs : 0);
   };
   const int64_t one = cost(1, stages);
   int split = 1, per_best = (int)stages;
   int64_t best = one;
-  for (int sl = 2; sl <= kMaxSplit && tiles * sl <= 256; ++sl) {
+  for (int sl = 2; sl <= kMaxSplit && (kF32 || tiles * sl <= 256); ++sl) {
     const int64_t per = (stages + sl - 1) / sl;
     if (per < 8) break;
     const int64_t slices = (stages + per - 1) / per;   // after rounding the slice up
