@@ -360,6 +360,56 @@ def bench_attention(stream, dnn, steps, warmup, cpu):
     return out
 
 
+SGEMM_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096, 4096, 4096),
+                (6144, 6144, 6144), (8192, 8192, 4096), (1024, 1024, 8192), (2048, 2048, 8192),
+                (4096, 4096, 1024), (4000, 4100, 1000)]
+
+
+def sgemm_shapes(steps: int) -> int:
+    """grxblasSgemm (N, N, column-major, alpha=1 beta=0, U[-0.5,0.5] inputs)
+    against torch's fp32 matmul of the same product, each timed after the
+    time-based warm-up, HIP/CUDA events around `steps` launches; the
+    library's output is checked against an fp64 product."""
+    import torch
+    g.load()
+    g.check_rt(g.load().rt.grxSetDevice(0), "grxSetDevice")
+    stream = g.Stream()
+    blas = g.Blas()
+    blas.set_stream(stream.s)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    for (m, n, k) in SGEMM_SHAPES:
+        a = torch.rand(k, m, device="cuda", generator=gen) - 0.5   # column-major m x k
+        b = torch.rand(n, k, device="cuda", generator=gen) - 0.5   # column-major k x n
+        c = torch.zeros(n, m, device="cuda")
+        torch.cuda.synchronize()
+        one, zero = g.fptr(1.0), g.fptr(0.0)
+        pa, pb, pc = a.data_ptr(), b.data_ptr(), c.data_ptr()
+
+        def launch():
+            st = blas.L.grxblasSgemm(blas.h, 0, 0, m, n, k, one, pa, m, pb, k, zero, pc, m)
+            if st != 0:
+                raise g.GrxError(f"Sgemm status {st}")
+        ms = time_launches(stream, launch, steps, None)
+        err = (c.double() - b.double() @ a.double()).abs().max().item()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_end = time.perf_counter() + WARM_SECONDS
+        while time.perf_counter() < t_end:
+            x = b @ a
+        e0.record()
+        for _ in range(steps):
+            x = b @ a
+        e1.record()
+        torch.cuda.synchronize()
+        tms = e0.elapsed_time(e1) / steps
+        del x
+        flops = 2.0 * m * n * k
+        print(json.dumps({"sgemm": [m, n, k], "layout": "N,N", "ms": round(ms, 4),
+                          "tflops": round(flops / ms / 1e9, 1), "torch_ms": round(tms, 4),
+                          "torch_tflops": round(flops / tms / 1e9, 1), "max_abs_err_vs_fp64": err}),
+              flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -368,6 +418,8 @@ def main() -> int:
                     help="untimed launches before each measurement (default: enough for %.2f s)" % WARM_SECONDS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention,sgemm,softmax,gelu")
+    ap.add_argument("--sgemm-shapes", action="store_true",
+                    help="print one JSON line per fp32 Sgemm shape (N,N): this library and torch's fp32 matmul")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy kernel of MIB MiB (torch), "
                          "the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -387,6 +439,8 @@ def main() -> int:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}).",
               file=sys.stderr)
         return 2
+    if args.sgemm_shapes:
+        return sgemm_shapes(args.steps)
     only = set(filter(None, args.only.split(",")))
     want = lambda n: not only or n in only  # noqa: E731
     cpu = not args.no_cpu_baseline
