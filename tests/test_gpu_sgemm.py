@@ -120,6 +120,57 @@ def test_sgemm_split_k_on_the_256_tile_kernel(blas, capfd):
         assert len(plans) == 1 and plans[0]["kernel"] == "tn256" and int(plans[0]["split"]) == 4, plans
 
 
+def test_large_sgemm_workspaces_on_many_streams(capfd):
+    """(N, N) Sgemm on the 256x256 kernel copies A into the workspace of the
+    calling stream: twelve calls rotating over six streams (more than the
+    handle keeps workspaces for, so workspaces are handed over) with no host
+    synchronisation between them, each bit-equal to the same call made alone
+    and synchronised, and the first of those within the gate's tolerance of
+    the oracle."""
+    m = n = 512
+    k, batch = 128, 64
+    blas = g.Blas()
+    streams = [g.Stream() for _ in range(6)]
+    try:
+        sets = []
+        for j in range(3):
+            A = O.fill_quarters(m * k * batch, 40 + j)
+            B = O.fill_quarters(k * n * batch, 50 + j)
+            sets.append((A, to_dev(A), B, to_dev(B)))
+        def call(j, dC):
+            _, dA, _, dB = sets[j]
+            return blas.sgemm_strided_batched(0, 0, m, n, k, 1.0, dA.p, m, m * k, dB.p, k, k * n, 0.0,
+                                              dC.p, m, m * n, batch)
+        from test_gpu_gemm import logged_plans
+        alone = []
+        for j in range(3):
+            dC = g.DeviceBuffer(m * n * batch * 4)
+            st = []
+            plans = logged_plans(capfd, lambda: st.append(call(j, dC)))
+            assert st == [g.SUCCESS]
+            assert len(plans) == 1 and plans[0]["kernel"] == "tn256" and plans[0]["copy_a"] == "1", plans
+            g.synchronize()
+            alone.append(dC.download(np.float32, m * n * batch))
+        A0, _, B0, _ = sets[0]
+        want = O.sgemm(0, 0, m, n, k, 1.0, A0, m, B0, k, 0.0, np.zeros(m * n, np.float32), m)
+        assert np.max(np.abs(alone[0][:m * n] - want)) <= 1e-5 * (k + 1)
+        outs = []
+        for i in range(12):
+            blas.set_stream(streams[i % 6].s)
+            dC = g.DeviceBuffer(m * n * batch * 4)
+            say(f"sgemm stream case {i}: set {i % 3} on stream {i % 6}")
+            assert call(i % 3, dC) == g.SUCCESS
+            outs.append(dC)
+        g.synchronize()
+        for i, dC in enumerate(outs):
+            got = dC.download(np.float32, m * n * batch)
+            assert np.array_equal(got.view(np.uint32), alone[i % 3].view(np.uint32)), i
+    finally:
+        blas.close()
+        for st in streams:
+            st.close()
+
+
 def test_config1_sgemm_512_cubed(blas):
     """fp32 C = A*B, 512^3 row-major, alpha=1 beta=0, U[-1,1]
     from seeds 1 and 2, mapped to column-major as C^T = B^T A^T:
