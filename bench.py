@@ -361,8 +361,9 @@ def bench_attention(stream, dnn, steps, warmup, cpu):
 
 
 SGEMM_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096, 4096, 4096),
-                (6144, 6144, 6144), (8192, 8192, 4096), (1024, 1024, 8192), (2048, 2048, 8192),
-                (4096, 4096, 1024), (4000, 4100, 1000)]
+                (4608, 4608, 4608), (5120, 5120, 5120), (6144, 6144, 6144), (8192, 8192, 4096),
+                (1024, 1024, 8192), (2048, 2048, 8192), (4096, 4096, 1024), (6144, 6144, 2048),
+                (4000, 4100, 1000)]
 
 
 def sgemm_shapes(steps: int) -> int:

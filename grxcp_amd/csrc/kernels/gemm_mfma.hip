@@ -888,6 +888,7 @@ struct Plan {
   int64_t ldw = 0;                // partials' leading dimension
   size_t w_bytes = 0;
   bool tn = false;                // the TN kernel runs (directly or on copies)
+  int64_t split_ns = 0;           // the split's modelled time (fp32 problems of 256+ tiles)
   GemmDesc e;                     // the TN problem (over the copies; ws unset)
   size_t bytes() const { return a_bytes + b_bytes + w_bytes; }
 };
@@ -943,27 +944,31 @@ Plan make_plan(const GemmDesc& d) {
   // kPartialBytesPerNs (mostly served from the last-level cache, hence above
   // the HBM rate).
   // fp32 stages are long enough (8x the MFMA work) that slices may also run
-  // in several waves of 256 workgroups: there the model charges ceil(tiles *
-  // s / 256) waves of ceil(stages/s) stages (3072^3: 144 tiles in 7 slices,
-  // 4 waves; 99 -> 109 TFLOP/s against the 128x128 kernel). Problems of 256
-  // tiles or more are not split (their alternative is that kernel, which
-  // finishes a partial last wave sooner than this model assumes).
+  // in several waves of 256 workgroups: there the model charges each wave
+  // its fill and drain (kFixNs) and ceil(stages/s) stages (3072^3: 144 tiles
+  // in 7 slices, 4 waves; 99 -> 114 TFLOP/s against the 128x128 kernel).
+  // fp32 problems of 256 tiles or more split only into slices of at least
+  // 32 stages (shorter ones measured slower than the model), and the caller
+  // takes such a split only where it beats the 128x128 kernel's best rate
+  // (fp32_mma_wanted).
   constexpr bool kF32 = std::is_same<Op, OpF32>::value;
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
   const int64_t stages = ((int64_t)d.k * EB + kFastKBytes - 1) / kFastKBytes;
-  if (tiles >= kSplitTiles || stages < 16) return t;
+  if ((!kF32 && tiles >= kSplitTiles) || stages < 16) return t;
+  const int64_t min_per = tiles >= kSplitTiles ? 32 : 8;
   const int64_t mn = ((int64_t)d.m + 7) / 8 * 8 * d.n;
   constexpr int64_t kStage = kF32 ? kStageNsF32 : kStageNs;
   auto cost = [&](int64_t sl, int64_t per) {
     const int64_t waves = kF32 ? (tiles * sl + 255) / 256 : 1;
-    return kFixNs + kStage * per * waves + (sl > 1 ? kReduceNs + 8 * sl * mn / kPartialBytesPerNs : 0);
+    return (kFixNs + kStage * per) * waves +
+           (sl > 1 ? kReduceNs + 8 * sl * mn / kPartialBytesPerNs : 0);
   };
   const int64_t one = cost(1, stages);
   int split = 1, per_best = (int)stages;
   int64_t best = one;
   for (int sl = 2; sl <= kMaxSplit && (kF32 || tiles * sl <= 256); ++sl) {
     const int64_t per = (stages + sl - 1) / sl;
-    if (per < 8) break;
+    if (per < min_per) break;
     const int64_t slices = (stages + per - 1) / per;   // after rounding the slice up
     const int64_t c = cost(slices, per);
     if (c < best) {
@@ -975,6 +980,7 @@ Plan make_plan(const GemmDesc& d) {
   if (split < 2 || best * 100 > one * 90) return t;
   const int kslice = per_best * (kFastKBytes / EB);
   t.split = split;
+  t.split_ns = best;
   t.kslice = kslice;
   t.k_last = d.k - (split - 1) * kslice;
   t.ldw = ((int64_t)d.m + 7) / 8 * 8;
@@ -1149,6 +1155,13 @@ bool fp32_mma_wanted(const GemmDesc& d) {
   const Plan t = make_plan<OpF32, MmaOut::F32>(d);
   if (!t.tn) return false;
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
+  if (t.split > 1 && tiles >= kSplitTiles) {
+    // A problem sgemm_mfma fills too: split only where the model beats that
+    // kernel's best rate, ~134 TFLOP/s (6144^3: 134 -> 140, 4608^3: 112 ->
+    // 132, 5120^3: 120 -> 132; 6144^2 x 2048 stays at 133, split 120).
+    const double flops = 2.0 * d.m * d.n * d.k;
+    return (double)t.split_ns * 134000.0 < flops;
+  }
   const int64_t units = tiles * d.batch * t.split;
   const int64_t waves = (units + 255) / 256;
   const int64_t last = units - (waves - 1) * 256;
