@@ -629,6 +629,151 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
 }
 
 // ---------------------------------------------------------------------------
+// TN path, 128x128 tiles
+// ---------------------------------------------------------------------------
+
+// For 16-bit and int8 TN problems with few 256x256 tiles and short K, where
+// neither one pass of gemm_tn_fast nor a split fills the GPU cheaply: 4 waves
+// of 64x64 (2x2 MFMA tiles each) per 128x128 tile, gemm_tn_fast's stage
+// layout and swizzle at half the rows (64 KB of LDS, two workgroups per CU),
+// a double-buffered K loop, C stored from registers in runs of 4 rows. The
+// DMA is issued as inline assembly: through the builtin, the compiler's
+// wait-count pass cannot tell the stage reads from the DMA still landing in
+// the other buffer and waits for all of it before every barrier.
+constexpr int kT128 = 128;
+
+template <class Op, MmaOut OUT>
+__global__ __launch_bounds__(256, 2) void gemm_tn128(KParams batch_p) {
+  constexpr int NS = 2;
+  const KParams p = batch_view(batch_p);
+  __shared__ __attribute__((aligned(1024))) i32x4 lds[2][NS][kT128 * kChunks];
+  const uint64_t t0 = p.probe ? cycle_now() : 0;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int tm, tn;
+  map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int row0 = tm * kT128, col0 = tn * kT128;
+  const int lda_b = (int)(p.lda * Op::kElemBytes);
+  const int ldb_b = (int)(p.ldb * Op::kElemBytes);
+  const int kbytes = p.k * Op::kElemBytes;
+  const int ktiles = (kbytes + kFastKBytes - 1) / kFastKBytes;
+  // Buffer descriptors as in gemm_tn_fast (record count ending at row m or
+  // n, so rows past the matrix read zero; offset 2^31 reads zero for a
+  // masked k chunk), as the four words the assembly takes.
+  const int rows_a = min(kT128, p.m - row0);
+  const int rows_b = min(kT128, p.n - col0);
+  constexpr uint32_t kOff = 0x80000000u;
+  auto rsrc_words = [&](const uint8_t* base, int bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    i32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xffff);
+    r[2] = __builtin_amdgcn_readfirstlane(bytes);
+    r[3] = (int)kRsrcWord3;
+    return r;
+  };
+  const i32x4 rsa = rsrc_words(p.a + (int64_t)row0 * lda_b, (rows_a - 1) * lda_b + kbytes);
+  const i32x4 rsb = rsrc_words(p.b + (int64_t)col0 * ldb_b, (rows_b - 1) * ldb_b + kbytes);
+  const int lr = lane >> 3, pc = lane & 7;
+  uint32_t base_a[4], base_b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int blk = 4 * i + wave;
+    const int row = 8 * blk + lr;
+    const int c = pc ^ lr ^ (blk & 7);
+    base_a[i] = (uint32_t)(row * lda_b + 16 * c);
+    base_b[i] = (uint32_t)(row * ldb_b + 16 * c);
+  }
+  auto dma = [&](int kt, int st) {
+    const int kb = kt * kFastKBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int blk = 4 * i + wave;
+      const int c = pc ^ lr ^ (blk & 7);
+      const bool ok = kb + 16 * c < kbytes;
+      const uint32_t va = ok ? base_a[i] + (uint32_t)kb : kOff;
+      const uint32_t vb = ok ? base_b[i] + (uint32_t)kb : kOff;
+      const uint32_t la = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][st][blk * 64];
+      const uint32_t lb = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[1][st][blk * 64];
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                   :: "s"(la), "v"(va), "s"(rsa) : "memory");
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                   :: "s"(lb), "v"(vb), "s"(rsb) : "memory");
+    }
+  };
+  using Acc = typename Op::Acc;
+  Acc acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  const int wm = wave >> 1, wn = wave & 1, r32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int q = 0; q < NS - 1; ++q)
+    if (q < ktiles) dma(q, q);
+  int st = 0;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    // stage kt+NS-1 is issued at the top so NS-1 stages are in flight
+    if (kt + NS - 1 < ktiles) {
+      int stn = st + NS - 1; if (stn >= NS) stn -= NS;
+      dma(kt + NS - 1, stn);
+    }
+    const int ahead = min(ktiles - 1 - kt, NS - 1);    // stages issued after kt
+    if (ahead >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    i32x4 fa[2][2], fb[2][2];
+    auto rd = [&](int ks, int b) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int ar = wm * 64 + 32 * t + r32;
+        const int br = wn * 64 + 32 * t + r32;
+        typedef __attribute__((address_space(3))) const i32x4* lds_frag_t;
+        const uint32_t l0 = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][0][0];
+        const uint32_t oa = 16u * (uint32_t)((0 * NS + st) * kT128 * kChunks + ar * kChunks + ((2 * ks + hh) ^ swz(ar)));
+        const uint32_t ob = 16u * (uint32_t)((1 * NS + st) * kT128 * kChunks + br * kChunks + ((2 * ks + hh) ^ swz(br)));
+        fa[b][t] = *(lds_frag_t)(uintptr_t)(l0 + oa);
+        fb[b][t] = *(lds_frag_t)(uintptr_t)(l0 + ob);
+      }
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks + 1 < 4) rd(ks + 1, (ks + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+    st = st + 1 == NS ? 0 : st + 1;
+  }
+  using E = typename Op::Elem;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int gj = col0 + wn * 64 + 32 * j + r32;
+      if (gj >= p.n) continue;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int i0 = row0 + wm * 64 + 32 * i + 8 * g + 4 * hh;
+        if (i0 >= p.m) continue;
+        const E v[4] = {(E)acc[i][j][4 * g], (E)acc[i][j][4 * g + 1], (E)acc[i][j][4 * g + 2],
+                        (E)acc[i][j][4 * g + 3]};
+        store_run<OUT>(p, i0, gj, v, 4, Epi<OUT>::kRun == 4);
+      }
+    }
+  cycle_record(p.probe, t0, probe_slot(wave), wave);
+}
+
+// ---------------------------------------------------------------------------
 // general path
 // ---------------------------------------------------------------------------
 
@@ -889,6 +1034,7 @@ struct Plan {
   size_t w_bytes = 0;
   bool tn = false;                // the TN kernel runs (directly or on copies)
   int64_t split_ns = 0;           // the split's modelled time (fp32 problems of 256+ tiles)
+  bool tn128 = false;             // the TN problem runs on 128x128 tiles (gemm_tn128)
   GemmDesc e;                     // the TN problem (over the copies; ws unset)
   size_t bytes() const { return a_bytes + b_bytes + w_bytes; }
 };
@@ -954,6 +1100,14 @@ Plan make_plan(const GemmDesc& d) {
   constexpr bool kF32 = std::is_same<Op, OpF32>::value;
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
   const int64_t stages = ((int64_t)d.k * EB + kFastKBytes - 1) / kFastKBytes;
+  // 16-bit and int8 problems of at least 1024 x 1024 with few 256x256 tiles
+  // and at most 32 stages of K: 128x128 tiles, one pass (2048^3 bf16: 470 ->
+  // 520 TFLOP/s against 3 slices; 1024^3 94 -> 111). Longer K keeps the
+  // 256x256 kernel (3072^3: 1026 against 574 on 128x128 tiles).
+  if (!kF32 && tiles < kSplitTiles && stages <= 32 && d.m >= 1024 && d.n >= 1024) {
+    t.tn128 = true;
+    return t;
+  }
   if ((!kF32 && tiles >= kSplitTiles) || stages < 16) return t;
   const int64_t min_per = tiles >= kSplitTiles ? 32 : 8;
   const int64_t mn = ((int64_t)d.m + 7) / 8 * 8 * d.n;
@@ -1035,7 +1189,7 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
                  "grxblas: gemm %s->%s ta=%d tb=%d m=%d n=%d k=%d batch=%d kernel=%s copy_a=%d "
                  "copy_b=%d split=%d\n",
                  Op::kName, out_name<OUT>(), (int)d.ta, (int)d.tb, d.m, d.n, d.k, d.batch,
-                 t.tn ? "tn256" : "general64", (int)t.copy_a, (int)t.copy_b, t.split);
+                 t.tn ? (t.tn128 ? "tn128" : "tn256") : "general64", (int)t.copy_a, (int)t.copy_b, t.split);
   }
 
   KParams p{};
@@ -1075,6 +1229,10 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     const int64_t items = (int64_t)((g->m + R - 1) / R) * g->n;
     hipLaunchKernelGGL((reduce_splits<OUT, E>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
                        p, (const E*)w, t.ldw, t.ldw * g->n, t.split);
+  } else if (t.tn && t.tn128) {
+    p.tiles_m = (g->m + kT128 - 1) / kT128;
+    p.tiles_n = (g->n + kT128 - 1) / kT128;
+    hipLaunchKernelGGL((gemm_tn128<Op, OUT>), dim3(p.tiles_m * p.tiles_n, g->batch), dim3(256), 0, s, p);
   } else if (t.tn) {
     p.tiles_m = (g->m + kFastTile - 1) / kFastTile;
     p.tiles_n = (g->n + kFastTile - 1) / kFastTile;

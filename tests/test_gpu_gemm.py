@@ -237,6 +237,39 @@ def test_split_k_plan_limits(blas, capfd):
         assert [p["split"] for p in plans] == [want], plans
 
 
+def test_tn128_path_exact(blas, capfd):
+    """16-bit and int8 problems of at least 1024 x 1024 with few 256x256 tiles
+    and at most 32 stages of K run on 128x128 tiles: every input/output
+    type, (T, N) directly and (N, N) behind the operand copy, ragged m and
+    K, alpha/beta, bit-exact against the oracle over the whole padded C,
+    with guard bands; the GRXBLAS_LOG line shows the path taken."""
+    cases = []
+    for ta, tb in ((1, 0), (0, 0)):
+        for it, ot in ((BF16, F32), (BF16, BF16), (F16, F16), (F16, F32)):
+            cases.append(("f", ta, tb, it, ot))
+        cases += [("i8", ta, tb, None, None), ("dq", ta, tb, None, None)]
+    bad = []
+    for kind, ta, tb, it, ot in cases:
+        # C columns and K rows on 16-byte boundaries; m, n and K ragged against the tiles
+        m, n, k = 1032, 1100, 200 if kind == "f" else 400
+        res = []
+        if kind == "f":
+            call = lambda: res.append(float_case(blas, it, ot, ta, tb, m, n, k, 1.5, -0.5, 0, 8,
+                                                 seed=7 + ta, guard=True))
+            ok = (0, 0)
+        elif kind == "i8":
+            call = lambda: res.append(int8_case(blas, ta, tb, m, n, k, 2.0, 1.0, 0, fill="rand", seed=9,
+                                                cpad=0, guard=True))
+            ok = 0
+        else:
+            call = lambda: res.append(dequant_case(blas, ta, tb, m, n, k, 0, 8, seed=11, guard=True))
+            ok = (0, 0)
+        plans = logged_plans(capfd, call)
+        if res != [ok] or len(plans) != 1 or plans[0]["kernel"] != "tn128":
+            bad.append((kind, ta, tb, it, ot, res, plans))
+    assert not bad, bad
+
+
 def test_split_k_workspaces_on_many_streams():
     """Split-K calls rotating over six streams (more than the handle keeps
     workspaces for per device, so workspaces are handed over) with no host
