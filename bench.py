@@ -93,6 +93,12 @@ def traffic_from_profiles(name: str):
         return None
 
 
+TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, per dispatch "
+                  "of this bench command (profiles/hbm_traffic.md), scaled by a plain copy kernel's "
+                  "readings; these count L2-to-fabric bytes, which include Infinity Cache hits, so "
+                  "they bound HBM traffic from above")
+
+
 def roofline(bound: str, work: float, ms: float, peak_key: str, traffic_key: str):
     if bound == "hbm":
         achieved = work / (ms * 1e-3) / 1e9      # GB/s
@@ -101,8 +107,10 @@ def roofline(bound: str, work: float, ms: float, peak_key: str, traffic_key: str
         achieved = work / (ms * 1e-3) / 1e12     # TFLOP/s (TOP/s for int8)
         unit = "TOP/s" if peak_key == "int8" else "TFLOP/s"
     peak = PEAK[peak_key]
+    traffic = traffic_from_profiles(traffic_key)
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(traffic_key)}
+            "frac": round(achieved / peak, 4), "traffic": traffic,
+            "traffic_source": TRAFFIC_SOURCE if traffic is not None else None}
 
 
 # ---- CPU baseline -------------------------------------------------------------
@@ -111,6 +119,24 @@ def cpu_threads() -> int:
     n = os.cpu_count() or 1
     cap = int(os.environ.get("OMP_NUM_THREADS", n))
     return max(1, min(n, cap))
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def with_host(d: dict) -> dict:
+    d["cpu_model"] = cpu_model()
+    d["host_cpus"] = os.cpu_count()
+    return d
 
 
 def cpu_gemm_baseline(A_bits, B_bits, M, N, K, target_s=10.0):
@@ -129,10 +155,10 @@ def cpu_gemm_baseline(A_bits, B_bits, M, N, K, target_s=10.0):
         spent += time.perf_counter() - t0
         done += r
     flops = 2.0 * done * N * K
-    return {"value": round(flops / spent / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+    return with_host({"value": round(flops / spent / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"{done} of {M} rows of M ({flops / 1e9:.1f} GFLOP) through the oracle's "
-                      f"fp32-accumulate GemmEx loop, {threads} OpenMP threads, {spent:.1f} s"}
+                      f"fp32-accumulate GemmEx loop, {threads} OpenMP threads, {spent:.1f} s"})
 
 
 def cpu_igemm_baseline(A, B, M, N, K, target_s=5.0):
@@ -147,8 +173,10 @@ def cpu_igemm_baseline(A, B, M, N, K, target_s=5.0):
         spent += time.perf_counter() - t0
         done += r
     ops = 2.0 * done * N * K
-    return {"value": round(ops / spent / 1e12, 6), "unit": "TOP/s", "cores": threads, "kind": "port",
-            "sample": f"{done} of {M} rows ({ops / 1e9:.1f} GOP), oracle int32 GEMM, {threads} threads"}
+    return with_host({"value": round(ops / spent / 1e12, 6), "unit": "TOP/s", "cores": threads,
+                      "kind": "port",
+                      "sample": f"{done} of {M} rows ({ops / 1e9:.1f} GOP), oracle int32 GEMM, "
+                                f"{threads} threads, {spent:.1f} s"})
 
 
 def cpu_norm_baseline(x_bits, gamma_bits, beta_bits, rows, hidden, layer):
@@ -165,8 +193,9 @@ def cpu_norm_baseline(x_bits, gamma_bits, beta_bits, rows, hidden, layer):
         O.rmsnorm(x, gf, 1e-6)
     dt = time.perf_counter() - t0
     moved = r * hidden * 4 + hidden * 2 * (2 if layer else 1)   # bf16 in + bf16 out
-    return {"value": round(moved / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{r} of {rows} rows, oracle fp64 norm, {threads} threads"}
+    return with_host({"value": round(moved / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+                      "kind": "port",
+                      "sample": f"{r} of {rows} rows, oracle fp64 norm, {threads} threads"})
 
 
 def cpu_attention_baseline(q, k, v, S, D, rows=256):
@@ -178,14 +207,15 @@ def cpu_attention_baseline(q, k, v, S, D, rows=256):
     O.attention_head(q, k, v, True, D ** -0.5, r0, S)
     dt = time.perf_counter() - t0
     flops = sum(4.0 * D * (i + 1) for i in range(r0, S))
-    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"one (b,h), last {rows} query rows ({flops / 1e9:.2f} GFLOP), oracle fp64, "
-                      f"{threads} threads"}
+    return with_host({"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+                      "kind": "port",
+                      "sample": f"one (b,h), last {rows} query rows ({flops / 1e9:.2f} GFLOP), "
+                                f"oracle fp64, {threads} threads"})
 
 
 # ---- GPU workloads --------------------------------------------------------------
 
-def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu):
+def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu, cpu_seconds=10.0):
     N = K = M
     log(f"bf16 GemmEx {M}^3: generating inputs")
     A = synth.normal_bf16(M * K, 21)
@@ -206,7 +236,7 @@ def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu):
            "unit": "TFLOP/s", "roofline": roofline("mfma", flops, ms, "bf16", f"gemm_bf16_{M}")}
     if cpu:
         log("bf16 GemmEx: CPU baseline")
-        out["cpu_baseline"] = cpu_gemm_baseline(A, B, M, N, K)
+        out["cpu_baseline"] = cpu_gemm_baseline(A, B, M, N, K, cpu_seconds)
     for d in (dA, dB, dC):
         d.close()
     return out
@@ -458,7 +488,7 @@ def main() -> int:
     if want("gemm"):
         headline = bench_gemm_bf16(stream, blas, 8192, args.steps, args.warmup, cpu)
     if want("gemm4096"):
-        ops.append(bench_gemm_bf16(stream, blas, 4096, args.steps, args.warmup, False))
+        ops.append(bench_gemm_bf16(stream, blas, 4096, args.steps, args.warmup, cpu, 5.0))
     if want("int8"):
         ops.append(bench_gemm_int8(stream, blas, args.steps, args.warmup, cpu))
     if want("rmsnorm"):

@@ -139,6 +139,23 @@ bool no_overlap(const grxdnnTensorStruct& t) {
   return true;
 }
 
+// Byte interval [lo, hi) covered by a tensor at p (strides are non-negative).
+struct Span { uintptr_t lo, hi; };
+Span span_of(const grxdnnTensorStruct& t, const void* p, size_t elem) {
+  int64_t last = 0;
+  for (int i = 0; i < t.nb; ++i)
+    if (t.dims[i] > 0) last += (int64_t)t.strides[i] * (t.dims[i] - 1);
+  const uintptr_t lo = (uintptr_t)p;
+  return {lo, lo + (uintptr_t)((last + 1) * (int64_t)elem)};
+}
+bool intersect(Span a, Span b) { return a.lo < b.hi && b.lo < a.hi; }
+
+bool same_strides(const grxdnnTensorStruct& a, const grxdnnTensorStruct& b) {
+  for (int i = 0; i < a.nb; ++i)
+    if (a.strides[i] != b.strides[i]) return false;
+  return true;
+}
+
 grxdnnStatus_t norm_common(grxdnnHandle_t handle, grxdnnTensorDescriptor_t xDesc, const void* x,
                            grxdnnTensorDescriptor_t wDesc, const void* gamma, const void* beta,
                            bool layer, float eps, grxdnnTensorDescriptor_t yDesc, void* y) {
@@ -421,6 +438,15 @@ grxdnnStatus_t grxdnnAttentionForward(grxdnnHandle_t handle, grxdnnAttentionDesc
   }
   if (!no_overlap(*oDesc)) return GRXDNN_STATUS_INVALID_VALUE;
   if (!q || !k || !v || !o) return GRXDNN_STATUS_INVALID_VALUE;
+  // A workgroup writes its O rows while workgroups of other query tiles of
+  // the same head still read K and V, so O may not overlap them. O == Q with
+  // the same layout is safe (a workgroup reads only its own Q rows, before it
+  // writes them); any other overlap with Q is refused too.
+  const Span so = span_of(*oDesc, o, 2);
+  if (intersect(so, span_of(*kDesc, k, 2)) || intersect(so, span_of(*vDesc, v, 2)))
+    return GRXDNN_STATUS_INVALID_VALUE;
+  if (intersect(so, span_of(*qDesc, q, 2)) && !(o == q && same_strides(*oDesc, *qDesc)))
+    return GRXDNN_STATUS_INVALID_VALUE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return GRXDNN_STATUS_NOT_SUPPORTED;
 

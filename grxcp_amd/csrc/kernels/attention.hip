@@ -59,8 +59,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // write: it would otherwise make every later transposing LDS read wait for
 // ALL outstanding DMA, including the prefetch of the next tile. Ordering is
 // explicit instead: each tile ends with s_waitcnt vmcnt(0) and a barrier
-// before any wave reads the stage this DMA fills. M0 carries the LDS base;
-// no other instruction in the attention kernel uses M0.
+// before any wave reads the stage this DMA fills. M0 carries the LDS base:
+// gfx950 needs one wait state between an M0 write and the LDS DMA that reads
+// it (the s_nop; the compiler's hazard pass does not look inside inline
+// assembly). M0 is a register the compiler reserves (a clobber naming it is
+// ignored), so each DMA writes it itself; in the gfx950 code of this kernel
+// and of gemm_tn128 no other instruction reads or writes M0.
 // s_waitcnt vmcnt(0) through the builtin, so that the compiler's own wait
 // bookkeeping also sees every earlier load as complete.
 __device__ __forceinline__ void wait_vmem_all() {
@@ -68,14 +72,14 @@ __device__ __forceinline__ void wait_vmem_all() {
   asm volatile("" ::: "memory");
 }
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :: "s"(lds), "v"(voff), "s"(rsrc) : "memory");
 }
 // The same with a wave-uniform byte offset in the instruction's soffset. The
 // buffer's range check sees only the per-lane offset, so this form is for
 // rows known to lie inside the tensor.
 __device__ __forceinline__ void dma16_so(i32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory");
 }
 

@@ -696,9 +696,11 @@ __global__ __launch_bounds__(256, 2) void gemm_tn128(KParams batch_p) {
       const uint32_t vb = ok ? base_b[i] + (uint32_t)kb : kOff;
       const uint32_t la = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][st][blk * 64];
       const uint32_t lb = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[1][st][blk * 64];
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+      // One wait state between the M0 write and the DMA that reads it (the
+      // hazard pass does not look inside inline assembly).
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                    :: "s"(la), "v"(va), "s"(rsa) : "memory");
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                    :: "s"(lb), "v"(vb), "s"(rsb) : "memory");
     }
   };

@@ -128,7 +128,10 @@ grxdnnStatus_t grxdnnGeluForward(grxdnnHandle_t handle, grxdnnGeluMode_t mode,
  * stride 1, with equal B, H, S and D. Supported head dimensions: 64, 128.
  * The other strides are multiples of 8 elements and the pointers 16-byte
  * aligned (else NOT_SUPPORTED); O's elements must not share addresses (else
- * INVALID_VALUE), while Q, K and V may (a broadcast).
+ * INVALID_VALUE), while Q, K and V may (a broadcast). O must not overlap K
+ * or V; it may be Q itself (same pointer, same strides: in place), and must
+ * not overlap Q otherwise (else INVALID_VALUE, checked on the address ranges
+ * the descriptors span).
  * Softmax and both products accumulate in fp32; O is rounded once (RNE). */
 grxdnnStatus_t grxdnnCreateAttentionDescriptor (grxdnnAttentionDescriptor_t* d);
 grxdnnStatus_t grxdnnDestroyAttentionDescriptor(grxdnnAttentionDescriptor_t d);

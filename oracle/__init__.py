@@ -55,10 +55,29 @@ _i8p = ctypes.POINTER(ctypes.c_int8)
 _i32p = ctypes.POINTER(ctypes.c_int32)
 
 
+REF_ROOT = "/root/reference"
+REF_DIR = os.path.join(_HERE, "_ref")
+HOST_BLAS = os.path.join(_HERE, "libgrxblas_ref.so")
+HOST_RT = os.path.join(_HERE, "libgrxrt_ref.so")
+
+
 def build() -> str:
-    """Compile the oracle with its Makefile (gcc). Returns the library path."""
+    """Compile the oracle and the CPU host backend (libgrxblas_ref.so,
+    libgrxrt_ref.so) with the Makefile (gcc). Returns the oracle's path."""
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
     return _LIB_PATH
+
+
+def build_ref() -> bool:
+    """Compile the reference's own grxBLAS callers (its three library gates
+    and its cycle benchmark) from their sources under /root/reference into
+    oracle/_ref/: once against the gfx950 libraries, once (the gates) against
+    the CPU host backend. Needs the product libraries built first. Returns
+    False, building nothing, where the reference is absent (the GPU box)."""
+    if not os.path.isdir(REF_ROOT):
+        return False
+    subprocess.run(["make", "-s", "-C", _HERE, "ref", f"REF={REF_ROOT}"], check=True)
+    return True
 
 
 def lib():

@@ -222,8 +222,40 @@ def test_attention_broadcast_input_passes_validation():
     q = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128])
     shared_rows = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128], [4096, 2048, 0, 1])
     bshd = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128], [4096, 128, 256, 1])
-    assert D.grxdnnAttentionForward(h, ad.d, shared_rows.d, FAKE, q.d, FAKE, q.d, FAKE, bshd.d,
-                                    FAKE) == g.ARCH_MISMATCH
+    fq, fk, fv, fo = (ctypes.c_void_p(0x100000 * (i + 1)) for i in range(4))
+    assert D.grxdnnAttentionForward(h, ad.d, shared_rows.d, fq, q.d, fk, q.d, fv, bshd.d,
+                                    fo) == g.ARCH_MISMATCH
+    # Q, K and V may overlap one another (here: the same buffer), and O may be
+    # Q itself with Q's layout (in place)
+    assert D.grxdnnAttentionForward(h, ad.d, q.d, fq, q.d, fq, q.d, fq, q.d, fo) == g.ARCH_MISMATCH
+    assert D.grxdnnAttentionForward(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, fq) == g.ARCH_MISMATCH
+    assert D.grxdnnDestroy(h) == g.SUCCESS
+
+
+def test_attention_output_overlapping_k_or_v_is_refused():
+    """A workgroup writes its O rows while workgroups of other query tiles of
+    the same head still read K and V: an O that overlaps K or V (or overlaps
+    Q other than as Q itself) would race, so validation refuses it."""
+    D = g.load().dnn
+    h = ctypes.c_void_p()
+    assert D.grxdnnCreate(ctypes.byref(h)) == g.SUCCESS
+    ad = g.AttnDesc(True, 0.125)
+    q = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128])           # 8 KB per tensor
+    bshd = g.TensorDesc(g.GRX_R_16BF, [1, 2, 16, 128], [4096, 128, 256, 1])
+    att = D.grxdnnAttentionForward
+    P = lambda a: ctypes.c_void_p(a)  # noqa: E731
+    fq, fk, fv = P(0x100000), P(0x200000), P(0x300000)
+    assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, fk) == g.INVALID_VALUE          # O == K
+    assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, fv) == g.INVALID_VALUE          # O == V
+    assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, P(0x300000 + 4096)) == g.INVALID_VALUE
+    assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, P(0x200000 - 4096)) == g.INVALID_VALUE
+    assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, P(0x100000 + 256)) == g.INVALID_VALUE
+    assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, bshd.d, fq) == g.INVALID_VALUE       # Q, other layout
+    # touching but not overlapping is fine (stops at the missing device, or runs)
+    ok = g.ARCH_MISMATCH if g.device_count() == 0 else None
+    if ok is not None:
+        assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, P(0x200000 + 8192)) == ok
+        assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, P(0x200000 - 8192)) == ok
     assert D.grxdnnDestroy(h) == g.SUCCESS
 
 

@@ -2,8 +2,9 @@
 
 Draws shapes, element types, row pitches, LayerNorm/RMSNorm, causal/full
 attention and both GELU forms from fixed seeds, and checks every call
-against the CPU oracle (the bounds of the targeted tests: norms 1e-2 in
-16-bit, 1e-5 in fp32; attention 1e-2 normwise per head; softmax and GELU
+against the CPU oracle (the bounds of the targeted tests: norms element-wise
+at half an output ulp plus fp32 arithmetic, with eps drawn too; attention
+1e-2 normwise per head; softmax and GELU
 element-wise at the output type's rounding, with the targeted tests'
 absolute floors). Every output buffer sits between two 4 KB guard bands
 filled with a byte pattern; a call that writes one byte outside its output
@@ -15,7 +16,7 @@ import pytest
 import grxcp_amd as g
 import oracle as O
 from helpers import Guarded, normwise_rel_err, say, to_dev
-from test_gpu_dnn import dec, enc, nptype
+from test_gpu_dnn import dec, enc, norm_violations, nptype
 from test_gpu_softmax_gelu import check
 
 pytestmark = pytest.mark.gpu
@@ -57,17 +58,17 @@ def test_norm_sweep(dnn):
         dx, dg, db, dy = to_dev(xbuf), to_dev(ge), to_dev(be), Guarded(poison)
         xd = g.TensorDesc(t, [rows, hidden], [pitch, 1])
         wd = g.TensorDesc(t, [hidden])
-        say(f"norm sweep {i}: layer={layer} t={t} rows={rows} hidden={hidden} pitch={pitch}")
-        s = (dnn.layernorm(xd, dx.p, wd, dg.p, db.p, 1e-6, xd, dy.p) if layer
-             else dnn.rmsnorm(xd, dx.p, wd, dg.p, 1e-6, xd, dy.p))
+        eps = float(_pick(r, [1e-6, 1e-6, 1e-5, 1e-3, 0.1, 1.0]))
+        say(f"norm sweep {i}: layer={layer} t={t} rows={rows} hidden={hidden} pitch={pitch} eps={eps}")
+        s = (dnn.layernorm(xd, dx.p, wd, dg.p, db.p, eps, xd, dy.p) if layer
+             else dnn.rmsnorm(xd, dx.p, wd, dg.p, eps, xd, dy.p))
         assert s == g.SUCCESS, g.STATUS[s]
         g.synchronize()
         got = dy.download(nptype(t)).reshape(rows, pitch)
         y = dec(np.ascontiguousarray(got[:, :hidden]), t)
         gq, bq = dec(ge, t), dec(be, t)
-        ref = O.layernorm(xq, gq, bq, 1e-6) if layer else O.rmsnorm(xq, gq, 1e-6)
-        tol = 1e-5 if t == F32 else 1e-2
-        ok = (np.max(np.abs(y - ref)) <= tol * max(1.0, np.max(np.abs(ref))) and dy.guards_intact()
+        ref = O.layernorm(xq, gq, bq, eps) if layer else O.rmsnorm(xq, gq, eps)
+        ok = (norm_violations(y, ref, bq if layer else None, t) == 0 and dy.guards_intact()
               and np.array_equal(got[:, hidden:].view(np.uint8), poison[:, hidden:].view(np.uint8)))
         if not ok:
             bad.append((i, t, layer, rows, hidden, pitch))

@@ -270,6 +270,36 @@ def test_tn128_path_exact(blas, capfd):
     assert not bad, bad
 
 
+@pytest.mark.parametrize("kind,it,ot,m,n,k", [
+    ("f", BF16, F32, 1030, 1100, 64),     # one K stage: the loop's first wait is its last
+    ("f", BF16, BF16, 1030, 1100, 64),
+    ("f", BF16, F32, 1024, 1056, 2048),   # exactly 32 stages, the plan's upper limit
+    ("f", F16, F16, 1030, 1024, 2048),
+    ("f", BF16, BF16, 1031, 1100, 200),   # m % 4 != 0: a partial run of rows per lane
+    ("f", F16, F32, 1029, 1060, 200),
+    ("i8", None, None, 1030, 1100, 128),  # int8: one 128-byte stage, and 32 of them
+    ("i8", None, None, 1030, 1100, 4096),
+])
+def test_tn128_stage_limits_and_ragged_rows(blas, capfd, kind, it, ot, m, n, k):
+    """gemm_tn128 at the ends of its K range (1 and 32 stages) and with m not
+    a multiple of 4, for fp32 and 16-bit C, bit-exact over the padded C with
+    guard bands; the plan must be the 128x128 kernel."""
+    res = []
+    if kind == "f":
+        # ldc = m + cpad keeps C columns on 16-byte boundaries
+        cpad = (-m) % 8 if ot != F32 else (-m) % 4
+        call = lambda: res.append(float_case(blas, it, ot, 1, 0, m, n, k, 1.0, 0.0, 0, cpad,  # noqa: E731
+                                             seed=k + m, guard=True))
+        ok = (0, 0)
+    else:
+        call = lambda: res.append(int8_case(blas, 1, 0, m, n, k, 1.0, 0.0, 0, fill="rand",  # noqa: E731
+                                            seed=k, cpad=(-m) % 4, guard=True))
+        ok = 0
+    plans = logged_plans(capfd, call)
+    assert res == [ok], res
+    assert len(plans) == 1 and plans[0]["kernel"] == "tn128", plans
+
+
 def test_split_k_workspaces_on_many_streams():
     """Split-K calls rotating over six streams (more than the handle keeps
     workspaces for per device, so workspaces are handed over) with no host
@@ -488,20 +518,34 @@ def test_bf16_random_normal_tolerance(blas):
         assert normwise_rel_err(got, ref) <= 1e-2
 
 
-def test_config2_bf16_8192_sampled(blas):
-    """BASELINE config 2 at full size: bf16 8192^3, TN (row-major A x
-    column-major B), bf16 C. Sampled rows x columns against the fp64 oracle on
-    the same bf16 inputs, max relative error <= 1e-2; every output finite."""
+@pytest.mark.parametrize("size", [8192, 4096])
+def test_config2_bf16_sampled(blas, size):
+    """BASELINE config 2 at both of its sizes: bf16 8192^3 and 4096^3, TN
+    (row-major A x column-major B), bf16 C. Sampled rows x columns against the
+    fp64 oracle on the same bf16 inputs, max relative error <= 1e-2; every
+    output finite. At 4096^3 the whole matrix is also checked against numpy's
+    float64 product (an independent BLAS), normwise <= 1e-2 and per element
+    within bf16 rounding of the exact value plus the fp32 accumulation error."""
     from grxcp_amd import synth
-    M = N = K = 8192
+    M = N = K = size
     A = synth.normal_bf16(M * K, 21)   # op(A): row-major M x K  (grxBLAS: transa=T, lda=K)
     B = synth.normal_bf16(N * K, 22)   # column-major K x N      (transb=N, ldb=K)
     dA, dB, dC = to_dev(A), to_dev(B), g.DeviceBuffer(M * N * 2)
-    say("config2 bf16 8192^3")
+    say(f"config2 bf16 {size}^3")
     assert blas.gemm_ex(1, 0, M, N, K, 1.0, dA.p, BF16, K, dB.p, BF16, K, 0.0, dC.p, BF16, M) == 0
     g.synchronize()
     C = O.bf16_to_f32(dC.download(np.uint16, M * N)).reshape(N, M)   # C[j, i] (column-major)
     assert np.isfinite(C).all()
+    if size == 4096:
+        af = O.bf16_to_f32(A).reshape(M, K).astype(np.float64)
+        bf = O.bf16_to_f32(B).reshape(N, K).astype(np.float64)
+        full = bf @ af.T                                   # [j, i] like C
+        assert normwise_rel_err(C, full) <= 1e-2
+        # bf16 output: half an ulp (2^-9 relative) of rounding, plus fp32
+        # accumulation over K terms of magnitude |a||b| (~K * 2^-24 * sum|ab|)
+        bound = 2.0 ** -8 * np.abs(full) + K * 2.0 ** -23 * (np.abs(bf) @ np.abs(af).T)
+        assert np.all(np.abs(C - full) <= bound)
+        del af, bf, full, bound
     r = np.random.default_rng(0)
     rows = np.sort(np.concatenate([[0, 255, 256, M - 1], r.choice(M, 12, replace=False)]))
     cols = np.sort(np.concatenate([[0, 255, 256, N - 1], r.choice(N, 124, replace=False)]))

@@ -1,0 +1,59 @@
+"""The reference's own grxBLAS gates, unchanged, against the gfx950 library.
+
+oracle/_ref/ holds the reference's three library gates (ref
+tests/libs/test_grxblas.cpp, test_grxblas_ex.cpp, test_grxblas_l12.cpp) and
+its cycle benchmark (ref tests/bench/gemm_cycles.cpp), compiled from their
+sources under /root/reference by `make -C oracle ref` against include/ and
+linked to grxcp_amd/lib/libgrxblas.so (build() does this where the reference
+is present; the binaries travel to the GPU box, the reference does not). Each
+gate is self-checking: it compares the library against its own CPU reference
+and prints PASSED or FAILED. Here they run on the MI355X.
+"""
+import os
+import subprocess
+import sys
+
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GATES = ["test_grxblas", "test_grxblas_ex", "test_grxblas_l12"]
+
+
+def _exe(name):
+    path = os.path.join(O.REF_DIR, name)
+    if not os.path.exists(path) and not O.build_ref():
+        pytest.skip(f"{name} is not built (oracle/_ref is built where /root/reference is present)")
+    return path
+
+
+def _run(name):
+    print(f"reference gate {name}", flush=True)
+    r = subprocess.run([_exe(name)], capture_output=True, text=True, timeout=120)
+    sys.stdout.write(r.stdout[-4000:])
+    return r
+
+
+@pytest.mark.parametrize("name", GATES)
+def test_reference_gate_passes_on_mi355x(gpu, name):
+    r = _run(name)
+    assert r.returncode == 0, (r.returncode, r.stdout[-3000:], r.stderr[-2000:])
+    assert "PASSED (0 failures)" in r.stdout
+    assert "  FAIL" not in r.stdout
+    # the gate says which library it tested (ref test_grxblas.cpp:297-305)
+    if name == "test_grxblas":
+        assert "libgrxblas.so" in r.stdout
+
+
+def test_reference_cycle_benchmark_runs_on_mi355x(gpu):
+    """The cycle benchmark reads per-wave s_memtime slots through the
+    reference's grxCycleSlot ABI at every shape. Its exit gate compares
+    GRX-G100 model cycles (GemmEx <= 1/5 of sgemm's cycles per element); the
+    MI355X's tiny-shape cycles say nothing about that model, so only the
+    measurement checks are asserted here."""
+    r = _run("gemm_cycles")
+    assert r.returncode in (0, 1), (r.returncode, r.stderr[-2000:])
+    assert "ok    every shape produced a measurement" in r.stdout, r.stdout[-3000:]
+    assert "ok    the tensor path was measured at every shape" in r.stdout
