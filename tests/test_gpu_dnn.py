@@ -44,10 +44,12 @@ def nptype(t):
 
 # Per-element bound for the norms: |y - ref| <= OUT_REL * |ref| (half an output
 # ulp: 8 significant bits in bf16, 11 in fp16 -- 2^-10 keeps a margin -- and
-# 24 in fp32) + ARITH * (|ref - beta| + |beta|) (fp32 arithmetic on the two
-# terms before they cancel: mean, variance and scale reductions over the row
-# in fp32, one rsqrt, a multiply by gamma, an add of beta) + FLOOR (fp16's
-# subnormal spacing). ref is the fp64 oracle on the same rounded inputs.
+# 24 in fp32) + ARITH * (|ref - beta| + |beta| + rms_row(ref - beta)) (fp32
+# arithmetic: the mean, variance and scale are fp32 reductions over the row,
+# so their rounding is an error on the row's scale, which reaches even the
+# elements near the mean; then one rsqrt, a multiply by gamma and an add of
+# beta on the element's own terms) + FLOOR (fp16's subnormal spacing). ref is
+# the fp64 oracle on the same rounded inputs.
 OUT_REL = {BF16: 2.0 ** -8, F16: 2.0 ** -10, F32: 2.0 ** -24}
 ARITH = {BF16: 2.0 ** -16, F16: 2.0 ** -16, F32: 2.0 ** -18}
 FLOOR = {BF16: 0.0, F16: 2.0 ** -25, F32: 0.0}
@@ -56,7 +58,9 @@ FLOOR = {BF16: 0.0, F16: 2.0 ** -25, F32: 0.0}
 def norm_bound(ref, beta, t):
     ref = np.asarray(ref, np.float64)
     b = np.zeros_like(ref) if beta is None else np.broadcast_to(np.asarray(beta, np.float64), ref.shape)
-    return OUT_REL[t] * np.abs(ref) + ARITH[t] * (np.abs(ref - b) + np.abs(b)) + FLOOR[t]
+    d = ref - b
+    row_rms = np.sqrt(np.mean(d * d, axis=-1, keepdims=True))
+    return OUT_REL[t] * np.abs(ref) + ARITH[t] * (np.abs(d) + np.abs(b) + row_rms) + FLOOR[t]
 
 
 def norm_violations(y, ref, beta, t):
