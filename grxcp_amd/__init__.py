@@ -93,6 +93,9 @@ _BLAS = {
     "grxblasGemmEx": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, _FP,
                               c_void_p, c_int, c_int, c_void_p, c_int, c_int, _FP,
                               c_void_p, c_int, c_int]),
+    "grxblasGemmExNoAlloc": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, _FP,
+                                     c_void_p, c_int, c_int, c_void_p, c_int, c_int, _FP,
+                                     c_void_p, c_int, c_int]),
     "grxblasGemmStridedBatchedEx": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, _FP,
                                             c_void_p, c_int, c_int, c_longlong, c_void_p, c_int,
                                             c_int, c_longlong, _FP, c_void_p, c_int, c_int,
@@ -270,6 +273,11 @@ class Blas:
     def gemm_ex(self, ta, tb, m, n, k, alpha, A, atype, lda, B, btype, ldb, beta, C, ctype, ldc) -> int:
         return self.L.grxblasGemmEx(self.h, int(ta), int(tb), m, n, k, fptr(alpha), A, atype, lda,
                                     B, btype, ldb, fptr(beta), C, ctype, ldc)
+
+    def gemm_ex_noalloc(self, ta, tb, m, n, k, alpha, A, atype, lda, B, btype, ldb, beta, C, ctype,
+                        ldc) -> int:
+        return self.L.grxblasGemmExNoAlloc(self.h, int(ta), int(tb), m, n, k, fptr(alpha), A, atype,
+                                           lda, B, btype, ldb, fptr(beta), C, ctype, ldc)
 
     def gemm_strided_batched_ex(self, ta, tb, m, n, k, alpha, A, atype, lda, sa, B, btype, ldb, sb,
                                 beta, C, ctype, ldc, sc, batch) -> int:

@@ -233,15 +233,40 @@ grxblasStatus_t launch_gemm(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut ou
   return from_hip(e);
 }
 
+// The allocation-free form: the same plan with the library's static
+// per-device scratch (grxk::gemm_noalloc_scratch) in place of the handle's
+// workspace. Calls no hipMalloc/hipFree; a plan that needs more scratch
+// than the array holds is refused before anything is launched.
+grxblasStatus_t launch_gemm_noalloc(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut out,
+                                    grxk::GemmDesc& d) {
+  const size_t need = grxk::gemm_workspace_bytes(in, out, d);
+  if (need > grxk::kNoAllocScratchBytes) {
+    std::fprintf(stderr,
+                 "grxblas: grxblasGemmExNoAlloc: this problem needs %zu bytes of scratch "
+                 "(operand copies / split-K partials), more than the %zu bytes the library "
+                 "holds per device; call grxblasGemmEx instead.\n",
+                 need, grxk::kNoAllocScratchBytes);
+    return GRXBLAS_STATUS_NOT_SUPPORTED;
+  }
+  if (need > 0) {
+    void* ws = grxk::gemm_noalloc_scratch();
+    if (!ws) return GRXBLAS_STATUS_INTERNAL_ERROR;
+    d.ws = ws;
+    d.ws_bytes = grxk::kNoAllocScratchBytes;
+  }
+  return from_hip(grxk::launch_mma_gemm(in, out, d, ctx.stream));
+}
+
 // GemmEx and its strided batch. Validation order of ref
 // src/libs/grxblas/grxblas.cpp:507-524, the batch count checked where
-// SgemmStridedBatched checks it.
+// SgemmStridedBatched checks it. no_alloc: grxblasGemmExNoAlloc.
 grxblasStatus_t gemm_ex_batched(grxblasHandle_t handle, grxblasOperation_t transa,
                                 grxblasOperation_t transb, int m, int n, int k,
                                 const float* alpha, const void* A, grxDataType_t Atype, int lda,
                                 long long strideA, const void* B, grxDataType_t Btype, int ldb,
                                 long long strideB, const float* beta, void* C,
-                                grxDataType_t Ctype, int ldc, long long strideC, int batch) {
+                                grxDataType_t Ctype, int ldc, long long strideC, int batch,
+                                bool no_alloc = false) {
   if (!handle) return GRXBLAS_STATUS_NOT_INITIALIZED;
   if (!alpha || !beta) return GRXBLAS_STATUS_INVALID_VALUE;
   if (m < 0 || n < 0 || k < 0) return GRXBLAS_STATUS_INVALID_VALUE;
@@ -294,6 +319,7 @@ grxblasStatus_t gemm_ex_batched(grxblasHandle_t handle, grxblasOperation_t trans
   d.probe = probe;
   d.batch = batch;
   d.stride_a = strideA; d.stride_b = strideB; d.stride_c = strideC;
+  if (no_alloc) return launch_gemm_noalloc(*handle, in, out, d);
   return launch_gemm(*handle, in, out, d);
 }
 
@@ -394,6 +420,15 @@ grxblasStatus_t grxblasGemmEx(grxblasHandle_t handle, grxblasOperation_t transa,
                               void* C, grxDataType_t Ctype, int ldc) {
   return gemm_ex_batched(handle, transa, transb, m, n, k, alpha, A, Atype, lda, 0, B, Btype,
                          ldb, 0, beta, C, Ctype, ldc, 0, 1);
+}
+
+grxblasStatus_t grxblasGemmExNoAlloc(grxblasHandle_t handle, grxblasOperation_t transa,
+                                     grxblasOperation_t transb, int m, int n, int k,
+                                     const float* alpha, const void* A, grxDataType_t Atype,
+                                     int lda, const void* B, grxDataType_t Btype, int ldb,
+                                     const float* beta, void* C, grxDataType_t Ctype, int ldc) {
+  return gemm_ex_batched(handle, transa, transb, m, n, k, alpha, A, Atype, lda, 0, B, Btype,
+                         ldb, 0, beta, C, Ctype, ldc, 0, 1, true);
 }
 
 grxblasStatus_t grxblasGemmStridedBatchedEx(grxblasHandle_t handle, grxblasOperation_t transa,

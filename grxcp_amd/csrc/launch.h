@@ -43,6 +43,11 @@ hipError_t launch_mma_gemm(MmaIn in, MmaOut out, const GemmDesc& d, hipStream_t 
 // Workspace bytes launch_mma_gemm would use for d (0: it needs none). With a
 // smaller d.ws_bytes the call takes the general path instead.
 size_t gemm_workspace_bytes(MmaIn in, MmaOut out, const GemmDesc& d);
+// Device address of the current device's scratch for grxblasGemmExNoAlloc
+// (kNoAllocScratchBytes, resolved once per device); null if it cannot be
+// resolved. Calls that overlap on one device share it, and race.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+void* gemm_noalloc_scratch();
 // fp32 problem d (MmaIn::F32 -> MmaOut::F32, no probe) that fills the GPU
 // with 256x256 tiles and can run the TN kernel, directly or behind copies.
 bool fp32_mma_wanted(const GemmDesc& d);

@@ -108,6 +108,28 @@ grxblasStatus_t grxblasGemmStridedBatchedEx(grxblasHandle_t handle,
                                             void* C, grxDataType_t Ctype, int ldc,
                                             long long strideC, int batchCount);
 
+/* new: grxblasGemmEx that allocates nothing. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, type triples, validation, status codes and results as
+ * grxblasGemmEx; where grxblasGemmEx would place transposed operand copies
+ * or split-K partials in a workspace the handle allocates, this call uses a
+ * static array of 64 MiB per device that the library holds until the
+ * process ends (resolved on the first call on each device). A problem that
+ * needs more scratch than that returns GRXBLAS_STATUS_NOT_SUPPORTED (with a
+ * one-line message) and launches nothing. Every call on one device shares
+ * that device's array: calls that overlap on one device (several streams or
+ * threads at once) race and give wrong results. */
+grxblasStatus_t grxblasGemmExNoAlloc(grxblasHandle_t handle,
+                                     grxblasOperation_t transa,
+                                     grxblasOperation_t transb,
+                                     int m, int n, int k,
+                                     const float* alpha,
+                                     const void* A, grxDataType_t Atype, int lda,
+                                     const void* B, grxDataType_t Btype, int ldb,
+                                     const float* beta,
+                                     void* C, grxDataType_t Ctype, int ldc);
+
 /* new: int8 GEMM with per-output-channel dequantisation.
  *
  *   acc[i,j] = sum_l op(A)[i,l] * op(B)[l,j]                 (exact, int32)

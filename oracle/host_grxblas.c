@@ -243,6 +243,18 @@ EXPORT grxblasStatus_t grxblasGemmEx(grxblasHandle_t handle, grxblasOperation_t 
                          0, beta, C, Ctype, ldc, 0, 1);
 }
 
+/* The host backend never allocates device memory, so the allocation-free
+ * form is GemmEx itself (its per-call host temporaries aside). */
+EXPORT grxblasStatus_t grxblasGemmExNoAlloc(grxblasHandle_t handle, grxblasOperation_t transa,
+                                            grxblasOperation_t transb, int m, int n, int k,
+                                            const float* alpha, const void* A, grxDataType_t Atype,
+                                            int lda, const void* B, grxDataType_t Btype, int ldb,
+                                            const float* beta, void* C, grxDataType_t Ctype,
+                                            int ldc) {
+  return gemm_ex_batched(handle, transa, transb, m, n, k, alpha, A, Atype, lda, 0, B, Btype, ldb,
+                         0, beta, C, Ctype, ldc, 0, 1);
+}
+
 EXPORT grxblasStatus_t grxblasGemmStridedBatchedEx(
     grxblasHandle_t handle, grxblasOperation_t transa, grxblasOperation_t transb, int m, int n,
     int k, const float* alpha, const void* A, grxDataType_t Atype, int lda, long long strideA,
