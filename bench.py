@@ -14,6 +14,13 @@ launches on the library handle's stream divided by K, after W untimed
 launches (default: as many as fill 0.25 s, at least 10; each line reports
 its count as "warmup").
 
+All inputs are generated and made resident in HBM first; the workloads then
+run back to back with no host work between them (the extras -- fp32 Sgemm,
+softmax, GELU -- first, the BASELINE configs after, the headline last), and
+the CPU baselines run after all GPU timing. The GPU idles at ~157 MHz and
+needs ~0.3 s of load to reach its operating clock (rocm-smi), so host work
+between workloads would put the next workload's first launches in that ramp.
+
 The CPU baseline (rank 0, N=1) times the oracle -- the reference's own CPU
 GEMM loop restated in C (ref tests/libs/test_grxblas_ex.cpp:45-63) -- on a
 bounded slice of the same workload on the host's cores.
@@ -214,8 +221,41 @@ def cpu_attention_baseline(q, k, v, S, D, rows=256):
 
 
 # ---- GPU workloads --------------------------------------------------------------
+#
+# Each prepare_* generates its inputs (seeded, on the host), uploads them and
+# returns a Workload: the launch closure, the algorithmic work per launch and
+# a CPU-baseline closure over the host copies it keeps. main() prepares every
+# selected workload first, then times them back to back (no host work between
+# them, so the GPU does not fall back to its idle clock: it idles at ~157 MHz
+# and takes ~0.3 s of load to reach its operating clock), then runs the CPU
+# baselines.
 
-def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu, cpu_seconds=10.0):
+class Workload:
+    def __init__(self, name, unit, bound, peak_key, traffic_key, work, launch, buffers,
+                 cpu=None, ms_digits=4):
+        self.name, self.unit, self.bound = name, unit, bound
+        self.peak_key, self.traffic_key, self.work = peak_key, traffic_key, work
+        self.launch, self.buffers, self.cpu, self.ms_digits = launch, buffers, cpu, ms_digits
+
+    def measure(self, stream, steps, warmup) -> dict:
+        log(f"{self.name}: timing")
+        ms = time_launches(stream, self.launch, steps, warmup)
+        scale = 1e6 if self.unit == "GB/s" else 1e9
+        return {"name": self.name, "ms": round(ms, self.ms_digits), "warmup": LAST_WARMUP[0],
+                "value": round(self.work / ms / scale, 2 if scale == 1e9 else 1), "unit": self.unit,
+                "roofline": roofline(self.bound, self.work, ms, self.peak_key, self.traffic_key)}
+
+    def close(self):
+        for d in self.buffers:
+            d.close()
+
+
+def _checked(status, what):
+    if status:
+        raise g.GrxError(f"{what} status {status}")
+
+
+def prepare_gemm_bf16(blas, M, cpu_seconds):
     N = K = M
     log(f"bf16 GemmEx {M}^3: generating inputs")
     A = synth.normal_bf16(M * K, 21)
@@ -224,25 +264,13 @@ def bench_gemm_bf16(stream, blas, M, steps, warmup, cpu, cpu_seconds=10.0):
     one, zero = g.fptr(1.0), g.fptr(0.0)
 
     def launch():
-        s = blas.L.grxblasGemmEx(blas.h, 1, 0, M, N, K, one, dA.p, BF16, K, dB.p, BF16, K, zero, dC.p,
-                                 BF16, M)
-        if s:
-            raise g.GrxError(f"GemmEx status {s}")
-    log(f"bf16 GemmEx {M}^3: timing")
-    ms = time_launches(stream, launch, steps, warmup)
-    flops = 2.0 * M * N * K
-    out = {"name": f"gemm_bf16_{M}", "ms": round(ms, 4), "warmup": LAST_WARMUP[0],
-           "value": round(flops / ms / 1e9, 2),
-           "unit": "TFLOP/s", "roofline": roofline("mfma", flops, ms, "bf16", f"gemm_bf16_{M}")}
-    if cpu:
-        log("bf16 GemmEx: CPU baseline")
-        out["cpu_baseline"] = cpu_gemm_baseline(A, B, M, N, K, cpu_seconds)
-    for d in (dA, dB, dC):
-        d.close()
-    return out
+        _checked(blas.L.grxblasGemmEx(blas.h, 1, 0, M, N, K, one, dA.p, BF16, K, dB.p, BF16, K, zero,
+                                      dC.p, BF16, M), "GemmEx")
+    return Workload(f"gemm_bf16_{M}", "TFLOP/s", "mfma", "bf16", f"gemm_bf16_{M}", 2.0 * M * N * K,
+                    launch, [dA, dB, dC], lambda: cpu_gemm_baseline(A, B, M, N, K, cpu_seconds))
 
 
-def bench_sgemm(stream, blas, steps, warmup):
+def prepare_sgemm(blas):
     """grxblasSgemm fp32 4096^3 (N, N, column-major), fp32 matrix-core roofline.
     The call copies A K-contiguous (transpose_k) and runs the 256x256-tile
     kernel; the timed region holds both."""
@@ -254,21 +282,12 @@ def bench_sgemm(stream, blas, steps, warmup):
     one, zero = g.fptr(1.0), g.fptr(0.0)
 
     def launch():
-        s = blas.L.grxblasSgemm(blas.h, 0, 0, M, N, K, one, dA.p, M, dB.p, K, zero, dC.p, M)
-        if s:
-            raise g.GrxError(f"Sgemm status {s}")
-    log("Sgemm 4096^3: timing")
-    ms = time_launches(stream, launch, steps, warmup)
-    flops = 2.0 * M * N * K
-    out = {"name": "sgemm_fp32_4096", "ms": round(ms, 4), "warmup": LAST_WARMUP[0],
-           "value": round(flops / ms / 1e9, 2),
-           "unit": "TFLOP/s", "roofline": roofline("mfma", flops, ms, "fp32", "sgemm_fp32_4096")}
-    for d in (dA, dB, dC):
-        d.close()
-    return out
+        _checked(blas.L.grxblasSgemm(blas.h, 0, 0, M, N, K, one, dA.p, M, dB.p, K, zero, dC.p, M), "Sgemm")
+    return Workload("sgemm_fp32_4096", "TFLOP/s", "mfma", "fp32", "sgemm_fp32_4096", 2.0 * M * N * K,
+                    launch, [dA, dB, dC])
 
 
-def bench_gemm_int8(stream, blas, steps, warmup, cpu):
+def prepare_gemm_int8(blas):
     M, K, N = 4096, 8192, 28672
     log("int8 GEMM + dequant: generating inputs")
     A = synth.uniform_int8(M * K, 31)
@@ -278,25 +297,14 @@ def bench_gemm_int8(stream, blas, steps, warmup, cpu):
     dS, dY = g.DeviceBuffer.from_array(scale), g.DeviceBuffer(M * N * 2)
 
     def launch():
-        s = blas.L.grxblasGemmExDequant(blas.h, 1, 0, M, N, K, dA.p, I8, K, dB.p, I8, K, dS.p, dY.p,
-                                        BF16, M)
-        if s:
-            raise g.GrxError(f"GemmExDequant status {s}")
-    log("int8 GEMM + dequant: timing")
-    ms = time_launches(stream, launch, steps, warmup)
-    ops = 2.0 * M * N * K
-    out = {"name": "gemm_int8_dequant_4096x28672x8192", "ms": round(ms, 4), "warmup": LAST_WARMUP[0],
-           "value": round(ops / ms / 1e9, 2), "unit": "TOP/s",
-           "roofline": roofline("mfma", ops, ms, "int8", "gemm_int8_dequant")}
-    if cpu:
-        log("int8: CPU baseline")
-        out["cpu_baseline"] = cpu_igemm_baseline(A, B, M, N, K)
-    for d in (dA, dB, dS, dY):
-        d.close()
-    return out
+        _checked(blas.L.grxblasGemmExDequant(blas.h, 1, 0, M, N, K, dA.p, I8, K, dB.p, I8, K, dS.p,
+                                             dY.p, BF16, M), "GemmExDequant")
+    w = Workload("gemm_int8_dequant_4096x28672x8192", "TOP/s", "mfma", "int8", "gemm_int8_dequant",
+                 2.0 * M * N * K, launch, [dA, dB, dS, dY], lambda: cpu_igemm_baseline(A, B, M, N, K))
+    return w
 
 
-def bench_norm(stream, dnn, layer, steps, warmup, cpu):
+def prepare_norm(dnn, layer):
     rows, hidden = 16384, 8192
     name = "layernorm" if layer else "rmsnorm"
     log(f"{name}: generating inputs")
@@ -314,24 +322,17 @@ def bench_norm(stream, dnn, layer, steps, warmup, cpu):
     def launch():
         i = state["i"] & 1
         state["i"] += 1
-        s = (dnn.layernorm(xd, dx[i].p, wd, dg.p, db.p, 1e-6, xd, dy[i].p) if layer
-             else dnn.rmsnorm(xd, dx[i].p, wd, dg.p, 1e-6, xd, dy[i].p))
-        if s:
-            raise g.GrxError(f"{name} status {s}")
-    log(f"{name}: timing")
-    ms = time_launches(stream, launch, steps, warmup)
+        _checked(dnn.layernorm(xd, dx[i].p, wd, dg.p, db.p, 1e-6, xd, dy[i].p) if layer
+                 else dnn.rmsnorm(xd, dx[i].p, wd, dg.p, 1e-6, xd, dy[i].p), name)
+    x0 = xs[0][: 2048 * hidden].copy()   # the CPU baseline's rows
+    del xs
     moved = rows * hidden * 2 * 2 + hidden * 2 * (2 if layer else 1)
-    out = {"name": f"{name}_16384x8192", "ms": round(ms, 5), "warmup": LAST_WARMUP[0],
-           "value": round(moved / ms / 1e6, 1),
-           "unit": "GB/s", "roofline": roofline("hbm", moved, ms, "hbm", name)}
-    if cpu:
-        out["cpu_baseline"] = cpu_norm_baseline(xs[0], gb, bb, rows, hidden, layer)
-    for d in dx + dy + [dg, db]:
-        d.close()
-    return out
+    return Workload(f"{name}_16384x8192", "GB/s", "hbm", "hbm", name, moved, launch,
+                    dx + dy + [dg, db], lambda: cpu_norm_baseline(x0, gb, bb, rows, hidden, layer),
+                    ms_digits=5)
 
 
-def bench_rowop(stream, dnn, op, steps, warmup):
+def prepare_rowop(dnn, op):
     """grxdnnSoftmaxForward / grxdnnGeluForward(tanh) on [16384, 8192] bf16."""
     rows, hidden = 16384, 8192
     log(f"{op}: generating inputs")
@@ -344,22 +345,13 @@ def bench_rowop(stream, dnn, op, steps, warmup):
     def launch():
         i = state["i"] & 1
         state["i"] += 1
-        s = (dnn.softmax(xd, dx[i].p, xd, dy[i].p) if op == "softmax"
-             else dnn.gelu(g.GELU_TANH, xd, dx[i].p, xd, dy[i].p))
-        if s:
-            raise g.GrxError(f"{op} status {s}")
-    log(f"{op}: timing")
-    ms = time_launches(stream, launch, steps, warmup)
-    moved = rows * hidden * 2 * 2
-    out = {"name": f"{op}_16384x8192", "ms": round(ms, 5), "warmup": LAST_WARMUP[0],
-           "value": round(moved / ms / 1e6, 1),
-           "unit": "GB/s", "roofline": roofline("hbm", moved, ms, "hbm", op)}
-    for d in dx + dy:
-        d.close()
-    return out
+        _checked(dnn.softmax(xd, dx[i].p, xd, dy[i].p) if op == "softmax"
+                 else dnn.gelu(g.GELU_TANH, xd, dx[i].p, xd, dy[i].p), op)
+    return Workload(f"{op}_16384x8192", "GB/s", "hbm", "hbm", op, rows * hidden * 2 * 2, launch,
+                    dx + dy, ms_digits=5)
 
 
-def bench_attention(stream, dnn, steps, warmup, cpu):
+def prepare_attention(dnn):
     B, H, S, D = 4, 32, 4096, 128
     n = B * H * S * D
     log("attention: generating inputs")
@@ -370,24 +362,16 @@ def bench_attention(stream, dnn, steps, warmup, cpu):
     ad = g.AttnDesc(True, D ** -0.5)
 
     def launch():
-        s = dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p)
-        if s:
-            raise g.GrxError(f"attention status {s}")
-    log("attention: timing")
-    ms = time_launches(stream, launch, steps, warmup)
-    flops = 4.0 * D * B * H * S * (S + 1) / 2
-    out = {"name": "attention_causal_b4h32s4096d128", "ms": round(ms, 4), "warmup": LAST_WARMUP[0],
-           "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
-           "roofline": roofline("mfma", flops, ms, "bf16", "attention")}
-    if cpu:
+        _checked(dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p), "attention")
+    q0, k0, v0 = (a[: S * D].copy() for a in (qb, kb, vb))   # the CPU baseline's head
+    del qb, kb, vb
+
+    def cpu():
         import oracle as O
-        q = O.bf16_to_f32(qb[: S * D]).reshape(S, D)
-        k = O.bf16_to_f32(kb[: S * D]).reshape(S, D)
-        v = O.bf16_to_f32(vb[: S * D]).reshape(S, D)
-        out["cpu_baseline"] = cpu_attention_baseline(q, k, v, S, D)
-    for d in (dq, dk, dv, do):
-        d.close()
-    return out
+        q, k, v = (O.bf16_to_f32(a).reshape(S, D) for a in (q0, k0, v0))
+        return cpu_attention_baseline(q, k, v, S, D)
+    return Workload("attention_causal_b4h32s4096d128", "TFLOP/s", "mfma", "bf16", "attention",
+                    4.0 * D * B * H * S * (S + 1) / 2, launch, [dq, dk, dv, do], cpu)
 
 
 SGEMM_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096, 4096, 4096),
@@ -483,26 +467,41 @@ def main() -> int:
     blas.set_stream(stream.s)
     dnn.set_stream(stream.s)
 
-    headline = None
-    ops = []
-    if want("gemm"):
-        headline = bench_gemm_bf16(stream, blas, 8192, args.steps, args.warmup, cpu)
-    if want("gemm4096"):
-        ops.append(bench_gemm_bf16(stream, blas, 4096, args.steps, args.warmup, cpu, 5.0))
-    if want("int8"):
-        ops.append(bench_gemm_int8(stream, blas, args.steps, args.warmup, cpu))
-    if want("rmsnorm"):
-        ops.append(bench_norm(stream, dnn, False, args.steps, args.warmup, cpu))
-    if want("layernorm"):
-        ops.append(bench_norm(stream, dnn, True, args.steps, args.warmup, cpu))
-    if want("attention"):
-        ops.append(bench_attention(stream, dnn, args.steps, args.warmup, cpu))
-    if want("sgemm"):
-        ops.append(bench_sgemm(stream, blas, args.steps, args.warmup))
-    if want("softmax"):
-        ops.append(bench_rowop(stream, dnn, "softmax", args.steps, args.warmup))
-    if want("gelu"):
-        ops.append(bench_rowop(stream, dnn, "gelu", args.steps, args.warmup))
+    # Reported order of the lines (BASELINE configs first), and the order the
+    # GPU runs them: the extras first, the BASELINE configs after, the
+    # headline last, back to back.
+    makers = {
+        "gemm": lambda: prepare_gemm_bf16(blas, 8192, 10.0),
+        "gemm4096": lambda: prepare_gemm_bf16(blas, 4096, 5.0),
+        "int8": lambda: prepare_gemm_int8(blas),
+        "rmsnorm": lambda: prepare_norm(dnn, False),
+        "layernorm": lambda: prepare_norm(dnn, True),
+        "attention": lambda: prepare_attention(dnn),
+        "sgemm": lambda: prepare_sgemm(blas),
+        "softmax": lambda: prepare_rowop(dnn, "softmax"),
+        "gelu": lambda: prepare_rowop(dnn, "gelu"),
+    }
+    report_order = ["gemm", "gemm4096", "int8", "rmsnorm", "layernorm", "attention", "sgemm",
+                    "softmax", "gelu"]
+    run_order = ["sgemm", "softmax", "gelu", "gemm4096", "int8", "rmsnorm", "layernorm",
+                 "attention", "gemm"]
+    selected = [k for k in report_order if want(k)]
+    loads = {k: makers[k]() for k in selected}          # inputs resident in HBM
+    g.synchronize()
+    results = {}
+    for k in run_order:
+        if k in loads:
+            results[k] = loads[k].measure(stream, args.steps, args.warmup)
+    if cpu:
+        for k in run_order:
+            w = loads.get(k)
+            if w is not None and w.cpu is not None:
+                log(f"{w.name}: CPU baseline")
+                results[k]["cpu_baseline"] = w.cpu()
+    for w in loads.values():
+        w.close()
+    headline = results.get("gemm")
+    ops = [results[k] for k in report_order if k in results and k != "gemm"]
 
     config = {"workload": "grxblasGemmEx bf16 M=N=K=8192, transa=T transb=N (row-major A x "
                           "column-major B), fp32 accumulate, bf16 C, alpha=1 beta=0",

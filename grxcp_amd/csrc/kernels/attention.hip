@@ -4,9 +4,14 @@
 // (ref docs/designs/grxcp_roadmap.md:864-877). Single pass, online softmax,
 // O(S) memory:
 //
-//  * one workgroup = 8 wavefronts (two per SIMD) = 256 query rows of one
-//    (batch, head); each wave owns 32 queries whose Q fragments stay in
-//    VGPRs for the whole pass;
+//  * persistent: one workgroup per CU (8 wavefronts, two per SIMD) loops
+//    over work items of 256 query rows of one (batch, head); each wave owns
+//    32 queries whose Q fragments stay in VGPRs for the item. The K/V double
+//    buffer runs across items (an item's last tile prefetches the next
+//    item's first), the next item's Q loads behind the last tile, and O is
+//    stored while the next item starts: no workgroup launch, prologue or
+//    drain between items (measured ~30K idle cycles per CU between one-shot
+//    workgroups, plus ~11K of prologue and epilogue);
 //  * K and V stream through LDS in 64-key tiles by direct-to-LDS buffer loads
 //    (no staging registers; rows past the sequence read as zero), double
 //    buffered, the next tile's loads in flight during the current tile;
@@ -25,10 +30,12 @@
 //    divided by the row sum once at the end and rounded once;
 //  * registers: this file is compiled with MFMA results in VGPRs
 //    (-amdgpu-mfma-vgpr-form), which keeps the scores, P and O out of
-//    AGPR<->VGPR copies (194 VGPRs, two waves per SIMD);
+//    AGPR<->VGPR copies (184 VGPRs, two waves per SIMD);
 //  * causal: key tiles past the query tile are never loaded; a 32-query block
-//    skips tiles entirely above its diagonal; workgroups run heaviest first,
-//    and all query tiles of a head run on one XCD (K/V shared in its L2).
+//    skips tiles entirely above its diagonal; heads are split over the XCDs
+//    (all query tiles of a head on one XCD: K/V shared in its L2) and each
+//    XCD's items are dealt heaviest first in a snake order, so every CU gets
+//    the same number of key tiles (272 of 69632 at B4 H32 S4096).
 
 #include "../launch.h"
 #include "device_common.h"
@@ -127,6 +134,7 @@ struct AParams {
   int64_t o_sb, o_sh, o_ss;
   int B, H, S;
   int qtiles;
+  int heads;      // B * H
   int causal;
   float c;  // scale * log2(e)
 };
@@ -156,16 +164,37 @@ __device__ __forceinline__ float half_swap_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// One work item = one (batch, head) and one tile of kBQ queries. Items are
+// split over the 8 XCDs by head (head h on XCD h % 8, so one head's K/V stay
+// in one L2); inside an XCD they are ordered heaviest first (causal: the
+// last query tiles) and dealt to the XCD's workgroups in a snake order,
+// round r going left to right for even r and right to left for odd r.
+struct ItemMap {
+  int xcd, wg, nwg;     // this workgroup's XCD, index within it, workgroups per XCD
+  int hx;               // heads on this XCD
+};
+__device__ __forceinline__ bool item_at(const AParams& p, const ItemMap& m, int round,
+                                        int* bh, int* qt) {
+  const int nloc = m.hx * p.qtiles;
+  const int k = (round & 1) ? (m.nwg - 1 - m.wg) : m.wg;
+  const int j = round * m.nwg + k;
+  if (j >= nloc || m.hx == 0) return false;
+  const int rank = j / m.hx;          // weight rank: 0 = heaviest
+  const int hl = j % m.hx;
+  *bh = m.xcd + 8 * hl;
+  *qt = p.causal ? (p.qtiles - 1 - rank) : rank;
+  return true;
+}
+
 template <AttnType T, int D>
 __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
   using IO = AIo<T>;
-  constexpr int CH = D / 8;            // 16-byte chunks per row
-  constexpr int RPI = 64 / CH;         // rows per 1 KB DMA instruction
-  constexpr int IPW = kBK / RPI / kNW; // DMA instructions per wave per tensor per tile
-  constexpr int DSTEPS = D / 16;       // MFMA k-steps over the head dim
-  constexpr int DT = D / 32;           // 32-wide output tiles over the head dim
+  constexpr int CH = D / 8;
+  constexpr int RPI = 64 / CH;
+  constexpr int IPW = kBK / RPI / kNW;
+  constexpr int DSTEPS = D / 16;
+  constexpr int DT = D / 32;
   static_assert(IPW >= 1, "tile too small for the wave count");
-  // [stage][K | V][key * CH + physical chunk]
   __shared__ __attribute__((aligned(1024))) i32x4 lds[2][2][kBK * CH];
 
   const int tid = threadIdx.x;
@@ -174,52 +203,13 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
-  // Work order: each XCD gets a contiguous run of logical ids (whole heads),
-  // and inside a head the longest (last) query tiles come first.
-  const int nb = gridDim.x;
-  int logical = blockIdx.x;
-  if ((nb & 7) == 0) logical = (blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3);
-  const int bh = logical / p.qtiles;
-  const int qt = p.causal ? (p.qtiles - 1 - logical % p.qtiles) : (logical % p.qtiles);
-  const int b = bh / p.H, h = bh % p.H;
-  const int q0 = qt * kBQ;
-  const int wq0 = q0 + 32 * wave;  // this wave's first query
+  ItemMap map;
+  map.xcd = blockIdx.x & 7;
+  map.wg = blockIdx.x >> 3;
+  map.nwg = gridDim.x >> 3;
+  map.hx = p.heads / 8 + (map.xcd < (p.heads & 7) ? 1 : 0);
 
-  const uint8_t* qg = p.q + 2 * (b * p.q_sb + h * p.q_sh);
-  const uint8_t* kg = p.k + 2 * (b * p.k_sb + h * p.k_sh);
-  const uint8_t* vg = p.v + 2 * (b * p.v_sb + h * p.v_sh);
-  uint8_t* og = p.o + 2 * (b * p.o_sb + h * p.o_sh);
-  // Byte pitches and offsets are unsigned 32-bit: the host guarantees one
-  // head's rows span < 2^31 bytes; padding rows past S wrap harmlessly into
-  // range checks that read zero.
   const uint32_t q_rs = (uint32_t)(2 * p.q_ss), k_rs = (uint32_t)(2 * p.k_ss), v_rs = (uint32_t)(2 * p.v_ss);
-
-  // Row-ranged buffer descriptors: rows past S read as zero.
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)qg, (short)0, (int)((uint32_t)(p.S - 1) * q_rs + 2 * D), kRsrcWord3);
-  const i32x4 rk = rsrc_words(kg, (uint32_t)(p.S - 1) * k_rs + 2 * D);
-  const i32x4 rv = rsrc_words(vg, (uint32_t)(p.S - 1) * v_rs + 2 * D);
-
-  // Q fragments (B operand of S^T = K Q^T): query wq0 + l32, head-dim
-  // elements 16*t + 8*hh .. +7.
-  const int myq = wq0 + l32;
-  i32x4 qf[DSTEPS];
-#pragma unroll
-  for (int t = 0; t < DSTEPS; ++t) {
-    qf[t] = __builtin_amdgcn_raw_buffer_load_b128(
-        rq, (uint32_t)myq * q_rs + (uint32_t)(2 * (16 * t + 8 * hh)), 0, 0);
-  }
-
-  const int kv_end = p.causal ? min(p.S, q0 + kBQ) : p.S;
-  const int ntiles = (kv_end + kBK - 1) / kBK;
-
-  // DMA: instruction i of wave w fills rows RPI*(IPW*w + i) .. of K or V;
-  // lane L lands in row +L/CH at physical chunk L%CH.
-  // The tile-invariant part of each DMA's offset (row within the tile and
-  // swizzled chunk). A tile whose rows all lie inside the sequence takes it
-  // with the tile's offset in soffset: no VALU work per DMA. The last,
-  // ragged tile and the prefetch past the end keep the masked form, whose
-  // per-lane offsets the buffer's range check turns into zeros.
   uint32_t kbase[IPW], vbase[IPW];
 #pragma unroll
   for (int i = 0; i < IPW; ++i) {
@@ -229,64 +219,100 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
     kbase[i] = (uint32_t)row * k_rs + (uint32_t)(16 * (pc ^ kswz<D>(row)));
     vbase[i] = (uint32_t)row * v_rs + (uint32_t)(16 * (pc ^ vswz<D>(row)));
   }
-  auto dma_tile = [&](int t, int st) {
+
+  // Per-item state: head pointers, buffer descriptors, tile count.
+  struct St {
+    int q0, ntiles;
+    const uint8_t* qg;
+    uint8_t* og;
+    i32x4 rk, rv;
+  };
+  auto setup = [&](int bh, int qt, St& s) {
+    const int b = bh / p.H, h = bh % p.H;
+    s.q0 = qt * kBQ;
+    s.qg = p.q + 2 * (b * p.q_sb + h * p.q_sh);
+    const uint8_t* kg = p.k + 2 * (b * p.k_sb + h * p.k_sh);
+    const uint8_t* vg = p.v + 2 * (b * p.v_sb + h * p.v_sh);
+    s.og = p.o + 2 * (b * p.o_sb + h * p.o_sh);
+    s.rk = rsrc_words(kg, (uint32_t)(p.S - 1) * k_rs + 2 * D);
+    s.rv = rsrc_words(vg, (uint32_t)(p.S - 1) * v_rs + 2 * D);
+    const int kv_end = p.causal ? min(p.S, s.q0 + kBQ) : p.S;
+    s.ntiles = (kv_end + kBK - 1) / kBK;
+  };
+  auto load_q = [&](const St& s, i32x4 (&qf)[DSTEPS]) {
+    const int myq = s.q0 + 32 * wave + l32;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)s.qg, (short)0, (int)((uint32_t)(p.S - 1) * q_rs + 2 * D), kRsrcWord3);
+#pragma unroll
+    for (int t = 0; t < DSTEPS; ++t)
+      qf[t] = __builtin_amdgcn_raw_buffer_load_b128(
+          rq, (uint32_t)myq * q_rs + (uint32_t)(2 * (16 * t + 8 * hh)), 0, 0);
+  };
+  // DMA of tile t of item s into LDS stage st (K and V).
+  auto dma_tile = [&](const St& s, int t, int st) {
     const int kv0 = t * kBK;
     if (kv0 + kBK <= p.S) {
       const uint32_t ks = (uint32_t)kv0 * k_rs, vs = (uint32_t)kv0 * v_rs;
 #pragma unroll
       for (int i = 0; i < IPW; ++i) {
         const int blk = IPW * wave + i;
-        dma16_so(rk, lds_addr(&lds[st][0][blk * 64]), kbase[i], ks);
-        dma16_so(rv, lds_addr(&lds[st][1][blk * 64]), vbase[i], vs);
+        dma16_so(s.rk, lds_addr(&lds[st][0][blk * 64]), kbase[i], ks);
+        dma16_so(s.rv, lds_addr(&lds[st][1][blk * 64]), vbase[i], vs);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < IPW; ++i) {
         const int blk = IPW * wave + i;
-        const bool ok = t < ntiles;
-        const uint32_t ko = ok ? (uint32_t)kv0 * k_rs + kbase[i] : 0x80000000u;
-        const uint32_t vo = ok ? (uint32_t)kv0 * v_rs + vbase[i] : 0x80000000u;
-        dma16(rk, lds_addr(&lds[st][0][blk * 64]), ko);
-        dma16(rv, lds_addr(&lds[st][1][blk * 64]), vo);
+        dma16(s.rk, lds_addr(&lds[st][0][blk * 64]), (uint32_t)kv0 * k_rs + kbase[i]);
+        dma16(s.rv, lds_addr(&lds[st][1][blk * 64]), (uint32_t)kv0 * v_rs + vbase[i]);
       }
     }
   };
+
+  int round = 0, bh = 0, qt = 0;
+  if (!item_at(p, map, round, &bh, &qt)) return;
+  St cur;
+  setup(bh, qt, cur);
+
+  i32x4 qf[DSTEPS];
+  load_q(cur, qf);
+  dma_tile(cur, 0, 0);
+  wait_vmem_all();
+  __syncthreads();
 
   f32x16 o_acc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.0f;
-  float m_run = -INFINITY;  // running max, scaled (log2) units
-  float l_run = 0.0f;       // this half-wave's share of the sum
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
 
-  dma_tile(0, 0);
-  wait_vmem_all();  // Q fragments and the first tile
-  __syncthreads();
-
-  // Transposed-read addressing for V^T (A operand of O^T = V^T P^T): lane l
-  // supplies head-dim row d = 32*dt + l32 and keys {16st + 4hh + r} (first
-  // read) and {16st + 8 + 4hh + r} (second read), r = 0..3. Source lane
-  // s = l%16 of its 16-lane group points at key 16st + 4hh + s/4 (+8),
-  // head-dim 32*dt + 16*((l>>4)&1) + 4*(s&3).
   const int tr_key = 4 * hh + ((lane & 15) >> 2);
   const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  // One 64-key tile; the LDS stage is a compile-time constant so every LDS
-  // address is a loop-invariant register plus an immediate offset.
-  auto tile = [&](auto stage, int t) {
-    constexpr int cur = decltype(stage)::value;
-    dma_tile(t + 1, cur ^ 1);
+  int t = 0;          // tile of the current item
+  bool done = false;
+  // One 64-key tile of the current item from LDS stage `stage`; the next
+  // tile (of this item, or tile 0 of the next one) loads into the other
+  // stage meanwhile. After an item's last tile its O is written, and the
+  // next item's Q has been loaded (issued right after the last scores).
+  auto tile = [&](auto stage) {
+    constexpr int cs = decltype(stage)::value;
+    const bool last = (t + 1 == cur.ntiles);
+    int nbh = 0, nqt = 0;
+    const bool have_next = last && item_at(p, map, round + 1, &nbh, &nqt);
+    St nxt;
+    if (have_next) setup(nbh, nqt, nxt);
+    if (!last) dma_tile(cur, t + 1, cs ^ 1);
+    else if (have_next) dma_tile(nxt, 0, cs ^ 1);
     const int kv0 = t * kBK;
-    const i32x4* kt = &lds[cur][0][0];
-    const uint8_t* vt = (const uint8_t*)&lds[cur][1][0];
-
-    // A wave whose 32 queries all precede this tile skips it (causal); the
-    // DMA it issued above and the barrier below are still its share.
+    const int wq0 = cur.q0 + 32 * wave;
+    const int myq = wq0 + l32;
+    const i32x4* kt = &lds[cs][0][0];
+    const uint8_t* vt = (const uint8_t*)&lds[cs][1][0];
     const bool wave_live = !p.causal || kv0 <= wq0 + 31;
     if (wave_live) {
-      // S^T tiles: [key block], 32 keys x 32 queries each. The K fragments
-      // of a key block are all read before its MFMAs.
       f32x16 s[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -299,9 +325,6 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
 #pragma unroll
         for (int d = 0; d < DSTEPS; ++d) s[kb] = IO::mma(kf[d], qf[d], s[kb]);
       }
-
-      // Keys past the sequence end, and (causal) past the query, are masked
-      // only on tiles that can contain such keys for this wave.
       const bool need_mask = (kv0 + kBK > p.S) || (p.causal && kv0 + kBK - 1 > wq0);
       if (need_mask) {
 #pragma unroll
@@ -313,8 +336,6 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
             s[kb][r] = masked ? -INFINITY : s[kb][r];
           }
       }
-
-      // Online softmax for this lane's query.
       uint32_t pk[2][8];
       {
         float mx0 = -INFINITY, mx1 = -INFINITY;
@@ -324,7 +345,6 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
           mx1 = fmaxf(mx1, s[1][r]);
         }
         const float mx = half_swap_max(fmaxf(mx0, mx1)) * p.c;
-        // Raise the running max only when this tile exceeds it by > 8.
         const bool raise = mx > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(raise)) {
           const float m_new = raise ? mx : m_run;
@@ -337,8 +357,6 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
             for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
         }
         const float m = m_run;
-        // The row sum adds the ROUNDED probabilities (v_dot2 over the packed
-        // pairs), the same values the O update multiplies.
         float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -352,8 +370,6 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
           }
         l_run += ps0 + ps1;
       }
-
-      // O^T += V^T P^T, 16 keys per MFMA step.
 #pragma unroll
       for (int st = 0; st < kBK / 16; ++st) {
         const int kb = st >> 1, half = st & 1;
@@ -362,7 +378,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
         const int k1 = 16 * st + tr_key, k2 = k1 + 8;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const int d = 32 * dt + tr_d;  // element column; 8-byte aligned
+          const int d = 32 * dt + tr_d;
           const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (lds_s16x4_t)(vt + k1 * (2 * D) + 16 * ((d >> 3) ^ vswz<D>(k1)) + 2 * (d & 7)));
           const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -373,30 +389,48 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
         }
       }
     }
-
-    wait_vmem_all();  // next tile's DMA landed
+    if (last) {
+      // O[q, d] = O^T[d, q] / l for this item; then start the next one.
+      const float l_tot = half_swap_sum(l_run);
+      const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+      if (myq < p.S) {
+        uint8_t* orow = cur.og + 2 * (int64_t)myq * p.o_ss;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d = dt * 32 + 8 * g + 4 * hh;
+            u32x2 w;
+            w.x = IO::pack2(o_acc[dt][4 * g + 0] * inv_l, o_acc[dt][4 * g + 1] * inv_l);
+            w.y = IO::pack2(o_acc[dt][4 * g + 2] * inv_l, o_acc[dt][4 * g + 3] * inv_l);
+            *(u32x2*)(orow + 2 * d) = w;
+          }
+      }
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.0f;
+      m_run = -INFINITY;
+      l_run = 0.0f;
+      if (have_next) {
+        load_q(nxt, qf);   // waited for below, with the next item's first tile
+        cur = nxt;
+        ++round;
+        t = 0;
+      } else {
+        done = true;
+      }
+    } else {
+      ++t;
+    }
+    wait_vmem_all();
     __syncthreads();
   };
-  for (int t = 0; t < ntiles; t += 2) {
-    tile(Stage<0>{}, t);
-    if (t + 1 < ntiles) tile(Stage<1>{}, t + 1);
-  }
-
-  // O[q, d] = O^T[d, q] / l; lane holds d = 32*dt + 8*g + 4*hh + 0..3.
-  const float l_tot = half_swap_sum(l_run);
-  const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (myq < p.S) {
-    uint8_t* orow = og + 2 * (int64_t)myq * p.o_ss;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = dt * 32 + 8 * g + 4 * hh;
-        u32x2 w;
-        w.x = IO::pack2(o_acc[dt][4 * g + 0] * inv_l, o_acc[dt][4 * g + 1] * inv_l);
-        w.y = IO::pack2(o_acc[dt][4 * g + 2] * inv_l, o_acc[dt][4 * g + 3] * inv_l);
-        *(u32x2*)(orow + 2 * d) = w;
-      }
+  while (true) {
+    tile(Stage<0>{});
+    if (done) break;
+    tile(Stage<1>{});
+    if (done) break;
   }
 }
 
@@ -411,16 +445,25 @@ hipError_t run(const AttnDesc& d, hipStream_t s) {
   p.o_sb = d.o_sb; p.o_sh = d.o_sh; p.o_ss = d.o_ss;
   p.B = d.B; p.H = d.H; p.S = d.S;
   p.qtiles = (d.S + kBQ - 1) / kBQ;
+  p.heads = d.B * d.H;
   p.causal = d.causal ? 1 : 0;
   p.c = d.scale * 1.4426950408889634f;
-  // 32-bit buffer offsets within one head: (S-1) * row pitch + row < 2^31.
   int64_t pitch = d.q_ss > d.k_ss ? d.q_ss : d.k_ss;
   pitch = pitch > d.v_ss ? pitch : d.v_ss;
   const int64_t span = ((int64_t)d.S + kBQ) * 2 * pitch + 2 * d.D;
   if (span >= (1ll << 31)) return hipErrorNotSupported;
-  const int64_t blocks = (int64_t)d.B * d.H * p.qtiles;
-  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_fwd<T, D>), dim3((unsigned)blocks), dim3(64 * kNW), 0, s, p);
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  // item indices are 32-bit in the kernel
+  if ((int64_t)d.B * d.H * p.qtiles > 0x7fffffff) return hipErrorInvalidValue;
+  // one workgroup per CU, a multiple of 8 (one share per XCD), no more than
+  // the items need
+  int64_t wgs = (cus / 8) * 8;
+  const int64_t per_xcd_items = ((int64_t)(p.heads + 7) / 8) * p.qtiles;
+  if (wgs / 8 > per_xcd_items) wgs = 8 * per_xcd_items;
+  if (wgs < 8) wgs = 8;
+  hipLaunchKernelGGL((attn_fwd<T, D>), dim3((unsigned)wgs), dim3(64 * kNW), 0, s, p);
   return hipGetLastError();
 }
 
