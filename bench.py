@@ -425,6 +425,45 @@ def sgemm_shapes(steps: int) -> int:
     return 0
 
 
+def stream_ceiling(steps: int) -> int:
+    """Streaming rates of plain device kernels on the norms' footprint
+    (268 MB in, 268 MB out; two buffer sets alternated so reads come from
+    HBM, not the 256 MB Infinity Cache), each after a 0.25 s warm-up, HIP
+    events around `steps` launches: torch's copy_ (read + write), a read-only
+    sum and a write-only fill. One JSON line per kernel."""
+    import torch
+    n = 16384 * 8192
+    xs = [torch.randn(n, device="cuda").to(torch.bfloat16) for _ in range(2)]
+    ys = [torch.empty_like(x) for x in xs]
+    torch.cuda.synchronize()
+    kernels = {
+        "copy": (lambda i: ys[i].copy_(xs[i]), 2 * 2 * n),
+        "read_sum": (lambda i: xs[i].sum(dtype=torch.float32), 2 * n),
+        "write_fill": (lambda i: ys[i].fill_(1.0), 2 * n),
+    }
+    for name, (fn, nbytes) in kernels.items():
+        state = {"i": 0}
+
+        def launch():
+            fn(state["i"] & 1)
+            state["i"] += 1
+        t_end = time.perf_counter() + WARM_SECONDS
+        while time.perf_counter() < t_end:
+            launch()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        print(json.dumps({"stream": name, "bytes": nbytes, "ms": round(ms, 5),
+                          "GB/s": round(nbytes / ms / 1e6, 1),
+                          "of_8TBps": round(nbytes / ms / 1e6 / PEAK["hbm"], 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -435,10 +474,16 @@ def main() -> int:
     ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention,sgemm,softmax,gelu")
     ap.add_argument("--sgemm-shapes", action="store_true",
                     help="print one JSON line per fp32 Sgemm shape (N,N): this library and torch's fp32 matmul")
+    ap.add_argument("--stream-ceiling", action="store_true",
+                    help="print the streaming rates of plain device kernels (torch copy, read-only "
+                         "sum, fill) on the norms' 16384x8192 bf16 footprint: the ceiling the "
+                         "HBM-bound lines are compared against")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy kernel of MIB MiB (torch), "
                          "the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.stream_ceiling:
+        return stream_ceiling(args.steps)
     if args.calibration_copy:
         import torch
         n = args.calibration_copy * (1 << 20)
