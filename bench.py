@@ -28,6 +28,7 @@ bounded slice of the same workload on the host's cores.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -441,6 +442,16 @@ def stream_ceiling(steps: int) -> int:
         "read_sum": (lambda i: xs[i].sum(dtype=torch.float32), 2 * n),
         "write_fill": (lambda i: ys[i].fill_(1.0), 2 * n),
     }
+    # the HIP runtime's device-to-device copy (its own copy kernel), on the
+    # library's stream through grxMemcpyAsync
+    rt = g.load().rt
+    g.check_rt(rt.grxSetDevice(0), "grxSetDevice")
+    cstream = torch.cuda.current_stream().cuda_stream
+
+    def hip_copy(i):
+        g.check_rt(rt.grxMemcpyAsync(ys[i].data_ptr(), xs[i].data_ptr(), ctypes.c_size_t(2 * n), 3,
+                                     ctypes.c_void_p(cstream)), "grxMemcpyAsync")
+    kernels["hip_memcpy_d2d"] = (hip_copy, 2 * 2 * n)
     for name, (fn, nbytes) in kernels.items():
         state = {"i": 0}
 

@@ -109,6 +109,7 @@ struct KParams {
   int k_last;             // split-K: k of the last grid.y slice (0: every slice has k)
   const float* scale;
   grxCycleSlot* probe;
+  int group;              // tile-rows per group of the XCD-aware tile order
 };
 
 // ---------------------------------------------------------------------------
@@ -311,13 +312,17 @@ __device__ __forceinline__ int64_t probe_slot(int wave) {
 
 // XCD-aware tile order. Consecutive workgroup ids are dispatched round-robin
 // over the 8 XCDs; remapping gives each XCD a contiguous run of logical tiles,
-// and the logical order walks groups of 8 tile-rows so that neighbours share
-// A panels in that XCD's L2.
+// and the logical order walks groups of `kgroup` tile-rows (8 by default) so
+// that neighbours share A and B panels in that XCD's L2: 32 concurrent tiles
+// per XCD as 8 rows x 4 columns stream 12 operand panels per round, the
+// fewest for 32 tiles (8192^3 bf16: FETCH_SIZE 1.61 GB per launch against
+// 2.47 GB for 16 x 2 and 4.45 GB for 32 x 1, which cost 0 % and 4 % of the
+// rate: the L2 egress is not what bounds this kernel).
 __device__ __forceinline__ void map_tile(int bid, int nblocks, int tiles_m, int tiles_n,
-                                         int& tm, int& tn) {
+                                         int kgroup, int& tm, int& tn) {
   int logical = bid;
   if ((nblocks & 7) == 0) logical = (bid & 7) * (nblocks >> 3) + (bid >> 3);
-  constexpr int kGroup = 8;
+  const int kGroup = kgroup > 0 ? kgroup : 8;
   const int per_group = kGroup * tiles_n;
   const int group = logical / per_group;
   const int first_m = group * kGroup;
@@ -354,7 +359,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   int tm, tn;
-  map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, p.group, tm, tn);
   const int row0 = tm * kFastTile;
   const int col0 = tn * kFastTile;
 
@@ -653,7 +658,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tn128(KParams batch_p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int tm, tn;
-  map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, p.group, tm, tn);
   const int row0 = tm * kT128, col0 = tn * kT128;
   const int lda_b = (int)(p.lda * Op::kElemBytes);
   const int ldb_b = (int)(p.ldb * Op::kElemBytes);
@@ -1152,6 +1157,15 @@ inline bool log_plans() {
   return v && *v && !(v[0] == '0' && v[1] == 0);
 }
 
+// GRXBLAS_TILE_GROUP=n (1..64): tile-rows per group of the XCD-aware tile
+// order (map_tile); default 8. A tuning variable, read on every call.
+inline int tile_group() {
+  const char* v = std::getenv("GRXBLAS_TILE_GROUP");
+  if (!v || !*v) return 8;
+  const int g = std::atoi(v);
+  return (g >= 1 && g <= 64) ? g : 8;
+}
+
 template <MmaOut OUT>
 constexpr const char* out_name() {
   return OUT == MmaOut::F32 ? "f32" : OUT == MmaOut::I32 ? "i32" : OUT == MmaOut::F16 ? "f16"
@@ -1206,6 +1220,7 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   p.ialpha = g->ialpha; p.ibeta = g->ibeta;
   p.scale = g->scale;
   p.probe = g->probe;
+  p.group = tile_group();
   p.sa = g->stride_a * EB;
   p.sb = g->stride_b * EB;
   p.sc = g->stride_c * out_bytes<OUT>();
