@@ -33,9 +33,10 @@
 //    AGPR<->VGPR copies (184 VGPRs, two waves per SIMD);
 //  * causal: key tiles past the query tile are never loaded; a 32-query block
 //    skips tiles entirely above its diagonal; heads are split over the XCDs
-//    (all query tiles of a head on one XCD: K/V shared in its L2) and each
-//    XCD's items are dealt heaviest first in a snake order, so every CU gets
-//    the same number of key tiles (272 of 69632 at B4 H32 S4096).
+//    (all query tiles of a head on one XCD: K/V shared in its L2), each
+//    XCD's items are dealt a block of heads at a time, heaviest first, in a
+//    snake order, so every CU gets the same number of key tiles (272 of
+//    69632 at B4 H32 S4096) and an XCD's CUs share few heads' K/V at a time.
 
 #include "../launch.h"
 #include "device_common.h"
@@ -166,9 +167,14 @@ __device__ __forceinline__ float half_swap_sum(float x) {
 
 // One work item = one (batch, head) and one tile of kBQ queries. Items are
 // split over the 8 XCDs by head (head h on XCD h % 8, so one head's K/V stay
-// in one L2); inside an XCD they are ordered heaviest first (causal: the
-// last query tiles) and dealt to the XCD's workgroups in a snake order,
-// round r going left to right for even r and right to left for odd r.
+// in one L2). Inside an XCD, round r deals the items of the next block of
+// heads (as many heads as one round has workgroups for their query tiles:
+// 2 at 32 workgroups and 16 tiles), heaviest (causal: last) query tile
+// first, to the XCD's workgroups in a snake order, left to right for even r
+// and right to left for odd r: two rounds give every workgroup the same
+// number of key tiles, and the workgroups of an XCD share few heads' K/V at
+// a time (B4 H32 S4096: FETCH_SIZE 564 MB per launch, against 1420 MB when
+// a round took the heaviest tiles of all 16 heads of the XCD).
 struct ItemMap {
   int xcd, wg, nwg;     // this workgroup's XCD, index within it, workgroups per XCD
   int hx;               // heads on this XCD
@@ -179,8 +185,15 @@ __device__ __forceinline__ bool item_at(const AParams& p, const ItemMap& m, int 
   const int k = (round & 1) ? (m.nwg - 1 - m.wg) : m.wg;
   const int j = round * m.nwg + k;
   if (j >= nloc || m.hx == 0) return false;
-  const int rank = j / m.hx;          // weight rank: 0 = heaviest
-  const int hl = j % m.hx;
+  int hb = m.nwg / p.qtiles;          // heads per block
+  if (hb < 1) hb = 1;
+  if (hb > m.hx) hb = m.hx;
+  const int blk_items = hb * p.qtiles;
+  const int blk = j / blk_items;
+  const int r2 = j - blk * blk_items;
+  const int hb_here = min(hb, m.hx - blk * hb);   // the last block may hold fewer
+  const int rank = r2 / hb_here;                  // weight rank: 0 = heaviest
+  const int hl = blk * hb + r2 % hb_here;
   *bh = m.xcd + 8 * hl;
   *qt = p.causal ? (p.qtiles - 1 - rank) : rank;
   return true;
