@@ -6,15 +6,19 @@
 //
 //  * persistent: one workgroup per CU (8 wavefronts, two per SIMD) loops
 //    over work items of 256 query rows of one (batch, head); each wave owns
-//    32 queries whose Q fragments stay in VGPRs for the item. The K/V double
-//    buffer runs across items (an item's last tile prefetches the next
-//    item's first), the next item's Q loads behind the last tile, and O is
-//    stored while the next item starts: no workgroup launch, prologue or
-//    drain between items (measured ~30K idle cycles per CU between one-shot
-//    workgroups, plus ~11K of prologue and epilogue);
+//    32 queries whose Q fragments stay in VGPRs for the item. The K/V loads
+//    run across items (an item's last tiles load the next item's first),
+//    the next item's Q loads behind the last tile, and O is stored while
+//    the next item starts: no workgroup launch, prologue or drain between
+//    items (measured ~30K idle cycles per CU between one-shot workgroups,
+//    plus ~11K of prologue and epilogue);
 //  * K and V stream through LDS in 64-key tiles by direct-to-LDS buffer loads
-//    (no staging registers; rows past the sequence read as zero), double
-//    buffered, the next tile's loads in flight during the current tile;
+//    (no staging registers; rows past the sequence read as zero) into three
+//    stages, each tile's loads issued two tiles ahead of its use (three
+//    stages measured 2-3 % faster than two with the same waits);
+//  * the K fragments of the score MFMAs are read four MFMAs ahead of their
+//    use and the two 32-key accumulation chains alternate (pinned with
+//    sched_group_barrier; +4 %);
 //  * scores are computed TRANSPOSED, S^T = K Q^T (v_mfma_f32_32x32x16): per
 //    lane the accumulator holds 32 keys of ONE query, so the softmax row
 //    max/sum is an in-register reduction plus one exchange with lane^32;
@@ -30,7 +34,7 @@
 //    divided by the row sum once at the end and rounded once;
 //  * registers: this file is compiled with MFMA results in VGPRs
 //    (-amdgpu-mfma-vgpr-form), which keeps the scores, P and O out of
-//    AGPR<->VGPR copies (184 VGPRs, two waves per SIMD);
+//    AGPR<->VGPR copies (195 VGPRs, two waves per SIMD);
 //  * causal: key tiles past the query tile are never loaded; a 32-query block
 //    skips tiles entirely above its diagonal; heads are split over the XCDs
 //    (all query tiles of a head on one XCD: K/V shared in its L2), each
@@ -47,6 +51,9 @@ namespace {
 constexpr int kNW = 8;          // wavefronts per workgroup (two per SIMD)
 constexpr int kBQ = 32 * kNW;   // queries per workgroup, 32 per wave
 constexpr int kBK = 64;   // keys per tile
+constexpr int kNS = 3;    // K/V tile stages in LDS (96 KB at head dim 128)
+constexpr int kQkAhead = 4;  // K fragments read ahead of the score MFMAs
+static_assert(kNS == 3, "the tile loop below is unrolled for three stages");
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -208,7 +215,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
   constexpr int DSTEPS = D / 16;
   constexpr int DT = D / 32;
   static_assert(IPW >= 1, "tile too small for the wave count");
-  __shared__ __attribute__((aligned(1024))) i32x4 lds[2][2][kBK * CH];
+  __shared__ __attribute__((aligned(1024))) i32x4 lds[kNS][2][kBK * CH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -286,10 +293,33 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
   if (!item_at(p, map, round, &bh, &qt)) return;
   St cur;
   setup(bh, qt, cur);
+  // DMA pointer: tile pft of item pround (state pf), kNS-1 tiles ahead of
+  // the tile being computed, running on into the next items.
+  int pround = 0, pft = 0;
+  St pf = cur;
+  bool pvalid = true;
+  auto advance = [&]() {
+    if (++pft == pf.ntiles) {
+      int b2 = 0, q2 = 0;
+      if (item_at(p, map, pround + 1, &b2, &q2)) {
+        ++pround;
+        setup(b2, q2, pf);
+        pft = 0;
+      } else {
+        pvalid = false;
+      }
+    }
+  };
 
   i32x4 qf[DSTEPS];
   load_q(cur, qf);
-  dma_tile(cur, 0, 0);
+#pragma unroll
+  for (int s0 = 0; s0 < kNS - 1; ++s0) {
+    if (pvalid) {
+      dma_tile(pf, pft, s0);
+      advance();
+    }
+  }
   wait_vmem_all();
   __syncthreads();
 
@@ -306,19 +336,17 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
 
   int t = 0;          // tile of the current item
   bool done = false;
-  // One 64-key tile of the current item from LDS stage `stage`; the next
-  // tile (of this item, or tile 0 of the next one) loads into the other
-  // stage meanwhile. After an item's last tile its O is written, and the
-  // next item's Q has been loaded (issued right after the last scores).
+  // One 64-key tile of the current item from LDS stage `stage`, while the
+  // tile kNS-1 ahead (of this item or the next ones) loads into the stage
+  // the previous tile used. After an item's last tile its O is written and
+  // the next item's Q fragments are loaded.
   auto tile = [&](auto stage) {
     constexpr int cs = decltype(stage)::value;
     const bool last = (t + 1 == cur.ntiles);
-    int nbh = 0, nqt = 0;
-    const bool have_next = last && item_at(p, map, round + 1, &nbh, &nqt);
-    St nxt;
-    if (have_next) setup(nbh, nqt, nxt);
-    if (!last) dma_tile(cur, t + 1, cs ^ 1);
-    else if (have_next) dma_tile(nxt, 0, cs ^ 1);
+    if (pvalid) {
+      dma_tile(pf, pft, (cs + kNS - 1) % kNS);
+      advance();
+    }
     const int kv0 = t * kBK;
     const int wq0 = cur.q0 + 32 * wave;
     const int myq = wq0 + l32;
@@ -326,18 +354,39 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
     const uint8_t* vt = (const uint8_t*)&lds[cs][1][0];
     const bool wave_live = !p.causal || kv0 <= wq0 + 31;
     if (wave_live) {
+      // S^T for keys 0-31 and 32-63: two independent accumulation chains,
+      // issued alternately, with the K fragments read kQkAhead MFMAs ahead
+      // of their use (the schedule is pinned below: left to itself the
+      // compiler reads each fragment just before its MFMA and waits for it,
+      // 4-5 % slower).
       f32x16 s[2];
+      {
+        i32x4 kf[DSTEPS][2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int row = kb * 32 + l32;
-        i32x4 kf[DSTEPS];
+        for (int d = 0; d < DSTEPS; ++d)
 #pragma unroll
-        for (int d = 0; d < DSTEPS; ++d) kf[d] = kt[row * CH + ((2 * d + hh) ^ kswz<D>(row))];
+          for (int kb = 0; kb < 2; ++kb) {
+            const int row = kb * 32 + l32;
+            kf[d][kb] = kt[row * CH + ((2 * d + hh) ^ kswz<D>(row))];
+          }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int d = 0; d < DSTEPS; ++d) s[kb] = IO::mma(kf[d], qf[d], s[kb]);
+          for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < DSTEPS; ++d)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) s[kb] = IO::mma(kf[d][kb], qf[d], s[kb]);
       }
+      // instruction groups, in order: kQkAhead LDS reads, then alternately
+      // one MFMA and one read, then the last kQkAhead MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, kQkAhead, 0);
+#pragma unroll
+      for (int i = 0; i < 2 * DSTEPS - kQkAhead; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 0);
       const bool need_mask = (kv0 + kBK > p.S) || (p.causal && kv0 + kBK - 1 > wq0);
       if (need_mask) {
 #pragma unroll
@@ -386,8 +435,8 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
 #pragma unroll
       for (int st = 0; st < kBK / 16; ++st) {
         const int kb = st >> 1, half = st & 1;
-        const i32x4 pf = i32x4{(int)pk[kb][4 * half + 0], (int)pk[kb][4 * half + 1],
-                               (int)pk[kb][4 * half + 2], (int)pk[kb][4 * half + 3]};
+        const i32x4 pf4 = i32x4{(int)pk[kb][4 * half + 0], (int)pk[kb][4 * half + 1],
+                                (int)pk[kb][4 * half + 2], (int)pk[kb][4 * half + 3]};
         const int k1 = 16 * st + tr_key, k2 = k1 + 8;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
@@ -398,7 +447,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
               (lds_s16x4_t)(vt + k2 * (2 * D) + 16 * ((d >> 3) ^ vswz<D>(k2)) + 2 * (d & 7)));
           const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
           const i32x4 vf = i32x4{(int)w0.x, (int)w0.y, (int)w1.x, (int)w1.y};
-          o_acc[dt] = IO::mma(vf, pf, o_acc[dt]);
+          o_acc[dt] = IO::mma(vf, pf4, o_acc[dt]);
         }
       }
     }
@@ -425,9 +474,10 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
         for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.0f;
       m_run = -INFINITY;
       l_run = 0.0f;
-      if (have_next) {
-        load_q(nxt, qf);   // waited for below, with the next item's first tile
-        cur = nxt;
+      int nbh = 0, nqt = 0;
+      if (item_at(p, map, round + 1, &nbh, &nqt)) {
+        setup(nbh, nqt, cur);
+        load_q(cur, qf);   // waited for below, with the DMA
         ++round;
         t = 0;
       } else {
@@ -443,6 +493,8 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
     tile(Stage<0>{});
     if (done) break;
     tile(Stage<1>{});
+    if (done) break;
+    tile(Stage<2>{});
     if (done) break;
   }
 }
