@@ -20,6 +20,12 @@ softmax, GELU -- first, the BASELINE configs after, the headline last), and
 the CPU baselines run after all GPU timing. The GPU idles at ~157 MHz and
 needs ~0.3 s of load to reach its operating clock (rocm-smi), so host work
 between workloads would put the next workload's first launches in that ramp.
+For the same reason the GPU is first brought out of idle: before the first
+measurement every workload is launched in turn, one launch each, for
+--preheat seconds (default 0.5; 0 turns it off). Measured on one box with 5
+warm-up launches: the whole run otherwise sits in the ramp (causal attention
+938 TFLOP/s after the other workloads, 846 alone, against 995 after 0.25 s of
+its own launches). The line reports the pre-heat time as "preheat_s".
 
 The CPU baseline (rank 0, N=1) times the oracle -- the reference's own CPU
 GEMM loop restated in C (ref tests/libs/test_grxblas_ex.cpp:45-63) -- on a
@@ -52,6 +58,7 @@ def log(msg: str) -> None:
 
 
 WARM_SECONDS = 0.25   # auto warm-up: at least this much back-to-back work
+PREHEAT_SECONDS = 0.5  # all workloads in turn before the first measurement
 LAST_WARMUP = [0]     # warm-up launches of the latest measurement
 
 
@@ -87,6 +94,20 @@ def time_launches(stream: g.Stream, launch, steps: int, warmup: int | None) -> f
     e0.close()
     e1.close()
     return ms / steps
+
+
+def preheat(loads: list, seconds: float) -> int:
+    """Launch every workload once in turn, synchronising after each round,
+    until `seconds` have passed: takes the GPU from its idle clock to its
+    operating point under this mix. Returns the number of rounds."""
+    rounds = 0
+    t_end = time.perf_counter() + seconds
+    while loads and time.perf_counter() < t_end:
+        for w in loads:
+            w.launch()
+        g.synchronize()
+        rounds += 1
+    return rounds
 
 
 def traffic_from_profiles(name: str):
@@ -482,6 +503,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed launches before each measurement (default: enough for %.2f s)" % WARM_SECONDS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--preheat", type=float, default=PREHEAT_SECONDS,
+                    help="seconds of all workloads' launches in turn before the first measurement "
+                         "(default %.1f; 0: none)" % PREHEAT_SECONDS)
     ap.add_argument("--only", default="", help="comma list: gemm,gemm4096,int8,rmsnorm,layernorm,attention,sgemm,softmax,gelu")
     ap.add_argument("--sgemm-shapes", action="store_true",
                     help="print one JSON line per fp32 Sgemm shape (N,N): this library and torch's fp32 matmul")
@@ -544,6 +568,9 @@ def main() -> int:
     selected = [k for k in report_order if want(k)]
     loads = {k: makers[k]() for k in selected}          # inputs resident in HBM
     g.synchronize()
+    if args.preheat > 0:
+        rounds = preheat([loads[k] for k in run_order if k in loads], args.preheat)
+        log(f"pre-heat: {rounds} rounds of every workload in {args.preheat} s")
     results = {}
     for k in run_order:
         if k in loads:
@@ -575,6 +602,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": headline["warmup"],
+        "preheat_s": args.preheat,
         "ms_per_step": headline["ms"],
         "higher_is_better": True,
         "scaling": "weak",
