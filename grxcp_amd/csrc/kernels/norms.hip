@@ -56,14 +56,18 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // 6.2-6.3 TB/s, against 5.6-5.8 TB/s for one row per wavefront at these
 // lengths. Each statistic is one wave butterfly plus one barrier; the waves'
 // partials are summed in a fixed order, so every thread sees the same value.
-// A workgroup takes gridDim.x-strided rows (two each on large inputs) with
-// gamma and beta loaded once into registers: LayerNorm re-reading beta per
-// row ran 4-5 % behind RMSNorm on the same bytes; two rows per workgroup
-// took it from 5960 to 6040 GB/s at 16384 x 8192 (more rows per workgroup,
-// or the loads hoisted with one row per workgroup, measured slower). The
-// partials alternate between two LDS slots by row, so a wave still reading
-// one row's partials cannot see the next row's writes, and the loop needs no
-// barrier of its own.
+// A workgroup takes gridDim.x-strided rows with gamma and beta loaded once
+// into registers: LayerNorm takes two rows per workgroup on large inputs
+// (re-reading beta per row ran 4-5 % behind RMSNorm on the same bytes; two
+// rows per workgroup took it from 5960 to 6040 GB/s at 16384 x 8192; more
+// rows per workgroup, or the loads hoisted with one row per workgroup,
+// measured slower), RMSNorm one (two measured 0.7-0.9 % slower for it). At
+// that size gamma's per-workgroup read from L2 costs RMSNorm 3 % (a copy
+// without it: 6460 against 6270 GB/s); sharing it through LDS between the
+// two halves of a 1024-thread workgroup, or prefetching the next row's x,
+// measured slower. The partials alternate between two LDS slots by row, so
+// a wave still reading one row's partials cannot see the next row's writes,
+// and the loop needs no barrier of its own.
 template <NormType T, bool LAYER, int NT, int NQ>
 __global__ __launch_bounds__(NT) void norm_block(NParams p) {
   using IO = Io<T>;
@@ -284,10 +288,10 @@ hipError_t run(const NormDesc& d, hipStream_t s) {
                    al(d.x) && al(d.y) && al(d.gamma) && (!LAYER || al(d.beta));
   const int nchunks = d.hidden / V;
   const unsigned wgrid = (unsigned)std::min<int64_t>((d.rows + 3) / 4, 1 << 30);
-  // norm_block: two rows per workgroup where that still leaves at least four
-  // workgroups per CU
+  // norm_block: LayerNorm two rows per workgroup where that still leaves at
+  // least four workgroups per CU, RMSNorm one
   const unsigned bgrid =
-      d.rows >= 2048 ? (unsigned)std::min<int64_t>((d.rows + 1) / 2, 1 << 30) : grid;
+      LAYER && d.rows >= 2048 ? (unsigned)std::min<int64_t>((d.rows + 1) / 2, 1 << 30) : grid;
   if (vec && nchunks <= 64) {
     hipLaunchKernelGGL((norm_wave<T, LAYER, 1>), dim3(wgrid), dim3(256), 0, s, p);
   } else if (vec && nchunks <= 128) {
