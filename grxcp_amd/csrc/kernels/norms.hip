@@ -37,6 +37,7 @@ struct NParams {
   uint8_t* y;
   int64_t x_rs, y_rs;  // row strides, elements
   int64_t rows;
+  int rows_per_wg;     // norm_block: adjacent rows per workgroup
   int hidden;
   float eps;
 };
@@ -56,15 +57,15 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // 6.2-6.3 TB/s, against 5.6-5.8 TB/s for one row per wavefront at these
 // lengths. Each statistic is one wave butterfly plus one barrier; the waves'
 // partials are summed in a fixed order, so every thread sees the same value.
-// A workgroup takes gridDim.x-strided rows with gamma and beta loaded once
-// into registers: LayerNorm takes two rows per workgroup on large inputs
-// (re-reading beta per row ran 4-5 % behind RMSNorm on the same bytes; two
-// rows per workgroup took it from 5960 to 6040 GB/s at 16384 x 8192; more
-// rows per workgroup, or the loads hoisted with one row per workgroup,
-// measured slower), RMSNorm one (two measured 0.7-0.9 % slower for it). At
-// that size gamma's per-workgroup read from L2 costs RMSNorm 3 % (a copy
-// without it: 6460 against 6270 GB/s); sharing it through LDS between the
-// two halves of a 1024-thread workgroup, or prefetching the next row's x,
+// On large inputs a workgroup takes two adjacent rows, with gamma and beta
+// loaded once into registers (blocks of rows_per_wg rows, strided by the
+// grid). Measured at 16384 x 8192 bf16, five interleaved repeats: one row per
+// workgroup re-reads gamma (and beta) per row, and their per-workgroup read
+// from L2 costs 3 % (a copy without gamma: 6460 against 6270 GB/s); two rows
+// a grid stride apart took LayerNorm from 5960 to 6050 GB/s but RMSNorm
+// down 0.8 %; two adjacent rows: RMSNorm 6250 -> 6310, LayerNorm 6050 ->
+// 6120; four or eight rows per workgroup, sharing gamma through LDS between
+// the halves of a 1024-thread workgroup, or prefetching the next row's x
 // measured slower. The partials alternate between two LDS slots by row, so
 // a wave still reading one row's partials cannot see the next row's writes,
 // and the loop needs no barrier of its own.
@@ -95,7 +96,9 @@ __global__ __launch_bounds__(NT) void norm_block(NParams p) {
     braw[q] = (LAYER && c < nchunks) ? ((const u32x4*)p.beta)[c] : u32x4{0, 0, 0, 0};
   }
 
-  for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x, parity ^= 1) {
+  const int64_t rb = p.rows_per_wg;
+  for (int64_t base = (int64_t)blockIdx.x * rb; base < p.rows; base += (int64_t)gridDim.x * rb)
+  for (int64_t row = base, rend = min(p.rows, base + rb); row < rend; ++row, parity ^= 1) {
     const uint8_t* xrow = p.x + row * p.x_rs * (int64_t)(16 / V);
     uint8_t* yrow = p.y + row * p.y_rs * (int64_t)(16 / V);
     u32x4 raw[NQ];
@@ -288,10 +291,11 @@ hipError_t run(const NormDesc& d, hipStream_t s) {
                    al(d.x) && al(d.y) && al(d.gamma) && (!LAYER || al(d.beta));
   const int nchunks = d.hidden / V;
   const unsigned wgrid = (unsigned)std::min<int64_t>((d.rows + 3) / 4, 1 << 30);
-  // norm_block: LayerNorm two rows per workgroup where that still leaves at
-  // least four workgroups per CU, RMSNorm one
+  // norm_block: two adjacent rows per workgroup where that still leaves at
+  // least four workgroups per CU
+  p.rows_per_wg = d.rows >= 2048 ? 2 : 1;
   const unsigned bgrid =
-      LAYER && d.rows >= 2048 ? (unsigned)std::min<int64_t>((d.rows + 1) / 2, 1 << 30) : grid;
+      (unsigned)std::min<int64_t>((d.rows + p.rows_per_wg - 1) / p.rows_per_wg, 1 << 30);
   if (vec && nchunks <= 64) {
     hipLaunchKernelGGL((norm_wave<T, LAYER, 1>), dim3(wgrid), dim3(256), 0, s, p);
   } else if (vec && nchunks <= 128) {

@@ -174,11 +174,10 @@ def test_norm_block_paths(dnn, t, layer, rows, hidden):
 @pytest.mark.parametrize("t,rows,hidden,pitch", [
     (BF16, 4099, 8192, 8192), (BF16, 2048, 4104, 4112), (F32, 2051, 3000, 3000)])
 def test_norm_block_two_rows_per_workgroup(dnn, t, layer, rows, hidden, pitch):
-    """From 2048 rows on, LayerNorm's norm_block runs two rows per workgroup
+    """From 2048 rows on, norm_block runs two adjacent rows per workgroup
     with gamma and beta held in registers and the partial sums alternating
-    between two LDS slots (RMSNorm keeps one row per workgroup): every row
-    checked, odd row counts (the last workgroup has one row), a padded
-    pitch, bf16 and fp32."""
+    between two LDS slots: every row checked, odd row counts (the last
+    workgroup has one row), a padded pitch, bf16 and fp32."""
     y, ref, beta = run_norm(dnn, layer, t, rows, hidden, seed=rows + 7 * hidden, pitch=pitch)
     check_norm(y, ref, beta, t)
 
