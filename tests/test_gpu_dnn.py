@@ -273,6 +273,49 @@ def test_attention_closed_forms(dnn):
     assert normwise_rel_err(oc, vqc) <= 1e-2
 
 
+def test_attention_key_permutation_invariant(dnn):
+    """Keys and their values permuted together leave every row of full
+    attention unchanged, and the last row of causal attention (which sees
+    every key); only the summation order differs. The kernel's tiling puts
+    the permuted keys in different tiles, so this also checks that the
+    online softmax across tiles is order-independent."""
+    B, H, S, D = 1, 2, 320, 128
+    r = np.random.default_rng(21)
+    q, k, v = (r.standard_normal((B, H, S, D)).astype(np.float32) for _ in range(3))
+    perm = r.permutation(S)
+    for causal in (False, True):
+        o1, _, _, _ = run_attention(dnn, BF16, B, H, S, D, causal, seed=0, q=q, k=k, v=v)
+        o2, _, _, _ = run_attention(dnn, BF16, B, H, S, D, causal, seed=0, q=q,
+                                    k=np.ascontiguousarray(k[:, :, perm]),
+                                    v=np.ascontiguousarray(v[:, :, perm]))
+        rows = slice(None) if not causal else slice(S - 1, S)
+        assert normwise_rel_err(o2[:, :, rows], o1[:, :, rows].astype(np.float64)) <= 5e-3, causal
+
+
+def test_rmsnorm_scale_invariant_and_one_hot(dnn):
+    """RMSNorm(x * 2^k) == RMSNorm(x) up to eps (a power-of-two scale is exact
+    in bf16 and leaves every fp32 step's relative rounding unchanged), and a
+    one-hot row a*e_j gives gamma_j * a / sqrt(a^2/H + eps) at j and 0
+    elsewhere."""
+    rows, hidden = 6, 8192
+    r = np.random.default_rng(5)
+    x = r.standard_normal((rows, hidden)).astype(np.float32)
+    y1, _, _ = run_norm(dnn, False, BF16, rows, hidden, seed=8, x=x, eps=0.0)
+    y2, _, _ = run_norm(dnn, False, BF16, rows, hidden, seed=8, x=x * 16.0, eps=0.0)
+    assert np.array_equal(y1, y2)
+    oh = np.zeros((rows, hidden), np.float32)
+    js = [0, 1, 4095, 4096, 8190, 8191]
+    amps = [1.0, -3.0, 0.5, 7.25, -0.125, 100.0]
+    for i, (j, a) in enumerate(zip(js, amps)):
+        oh[i, j] = a
+    y, ref, _ = run_norm(dnn, False, BF16, rows, hidden, seed=9, x=oh, eps=1e-6)
+    check_norm(y, ref, None, BF16)
+    for i, j in enumerate(js):
+        assert np.count_nonzero(y[i]) == 1 and y[i, j] != 0
+        want = ref[i, j]
+        assert abs(y[i, j] - want) <= 2.0 ** -8 * abs(want)
+
+
 def test_attention_strided_layout(dnn):
     """[B, S, H, D] storage described by strides (heads interleaved)."""
     B, H, S, D = 2, 4, 192, 128
