@@ -15,7 +15,7 @@
 //  * K and V stream through LDS in 64-key tiles by direct-to-LDS buffer loads
 //    (no staging registers; rows past the sequence read as zero) into three
 //    stages, each tile's loads issued two tiles ahead of its use (three
-//    stages measured 2-3 % faster than two with the same waits);
+//    stages measured 0.7-2.7 % faster than two with the same waits);
 //  * the K fragments of the score MFMAs are read four MFMAs ahead of their
 //    use and the two 32-key accumulation chains alternate (pinned with
 //    sched_group_barrier; +4 %);
