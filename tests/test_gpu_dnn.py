@@ -273,6 +273,20 @@ def test_attention_closed_forms(dnn):
     assert normwise_rel_err(oc, vqc) <= 1e-2
 
 
+@pytest.mark.parametrize("B,H,S,D,causal", [(4, 256, 64, 128, True), (4, 256, 64, 64, False),
+                                             (2, 128, 300, 128, True), (1, 512, 100, 64, True)])
+def test_attention_many_items_per_workgroup(dnn, B, H, S, D, causal):
+    """Enough heads that every persistent workgroup runs several items, with
+    items of one or two tiles: the K/V loads issued two tiles ahead cross
+    into the next items, and each item's Q and O move at item boundaries.
+    Every head checked."""
+    o, q, k, v = run_attention(dnn, BF16, B, H, S, D, causal, seed=B * H + S + D)
+    for b in range(B):
+        for h in range(H):
+            ref = O.attention_head(q[b, h], k[b, h], v[b, h], causal, D ** -0.5)
+            assert normwise_rel_err(o[b, h], ref) <= 1e-2, (b, h)
+
+
 def test_attention_key_permutation_invariant(dnn):
     """Keys and their values permuted together leave every row of full
     attention unchanged, and the last row of causal attention (which sees
