@@ -31,10 +31,12 @@
 //    exceeds it by more than 8 (p <= 2^8 otherwise, exact in bf16's relative
 //    precision), so the O rescale (and its 128 multiplies) is rare;
 //  * P is packed with v_cvt_pk_bf16_f32 (round to nearest even); O is
-//    divided by the row sum once at the end and rounded once;
+//    divided by the row sum once at the end, rounded once, and leaves
+//    through a per-wave LDS region as whole rows (not 8-byte pieces of 32
+//    rows per store instruction);
 //  * registers: this file is compiled with MFMA results in VGPRs
 //    (-amdgpu-mfma-vgpr-form), which keeps the scores, P and O out of
-//    AGPR<->VGPR copies (195 VGPRs, two waves per SIMD);
+//    AGPR<->VGPR copies (226 VGPRs, two waves per SIMD);
 //  * causal: key tiles past the query tile are never loaded; a 32-query block
 //    skips tiles entirely above its diagonal; heads are split over the XCDs
 //    (all query tiles of a head on one XCD: K/V shared in its L2), each
@@ -216,6 +218,10 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
   constexpr int DT = D / 32;
   static_assert(IPW >= 1, "tile too small for the wave count");
   __shared__ __attribute__((aligned(1024))) i32x4 lds[kNS][2][kBK * CH];
+  // Each wave's O tile (32 rows of D values) passes through here on its way
+  // out, so that every global store writes whole rows (8 KB per wave at
+  // D = 128; 160 KB of LDS in all).
+  __shared__ __attribute__((aligned(1024))) i32x4 ost[kNW][32 * CH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -455,18 +461,41 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
       // O[q, d] = O^T[d, q] / l for this item; then start the next one.
       const float l_tot = half_swap_sum(l_run);
       const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-      if (myq < p.S) {
-        uint8_t* orow = cur.og + 2 * (int64_t)myq * p.o_ss;
+      // A lane holds 4-value pieces of its query's row, 16 of them spread
+      // over the row; stored as they are, one instruction writes 8 bytes in
+      // each of 32 rows. Instead the wave parks the rounded tile in its LDS
+      // region ([row][16-byte chunk], chunk XOR row) and reads it back as
+      // whole rows, RPI rows per instruction (+1.5-2.2 %; non-temporal
+      // stores measured the same).
+      {
+        uint8_t* my = (uint8_t*)&ost[wave][0];
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const int d = dt * 32 + 8 * g + 4 * hh;
+            const int c = (4 * dt + g) ^ (l32 & (CH - 1));
             u32x2 w;
             w.x = IO::pack2(o_acc[dt][4 * g + 0] * inv_l, o_acc[dt][4 * g + 1] * inv_l);
             w.y = IO::pack2(o_acc[dt][4 * g + 2] * inv_l, o_acc[dt][4 * g + 3] * inv_l);
-            *(u32x2*)(orow + 2 * d) = w;
+            *(u32x2*)(my + 16 * (l32 * CH + c) + 8 * hh) = w;
           }
+        // LDS operations of one wave complete in order; the compiler only
+        // must not move the reads above the writes.
+        asm volatile("" ::: "memory");
+        const int rr = lane / CH, cc = lane % CH;
+        // Rows at or past S lie outside the descriptor's range: the buffer
+        // store drops them.
+        const uint32_t o_rs = (uint32_t)(2 * p.o_ss);
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)cur.og, (short)0, (int)((uint32_t)(p.S - 1) * o_rs + 2 * D), kRsrcWord3);
+        const uint32_t vo = (uint32_t)(cur.q0 + 32 * wave + rr) * o_rs + 16 * cc;
+#pragma unroll
+        for (int i = 0; i < 32 / RPI; ++i) {
+          const int r = RPI * i + rr;
+          const i32x4 v = *(const i32x4*)(my + 16 * (r * CH + (cc ^ (r & (CH - 1)))));
+          __builtin_amdgcn_raw_buffer_store_b128(v, ro, vo + (uint32_t)(RPI * i) * o_rs, 0, 0);
+        }
+        asm volatile("" ::: "memory");
       }
 #pragma unroll
       for (int i = 0; i < DT; ++i)
@@ -513,8 +542,10 @@ hipError_t run(const AttnDesc& d, hipStream_t s) {
   p.heads = d.B * d.H;
   p.causal = d.causal ? 1 : 0;
   p.c = d.scale * 1.4426950408889634f;
+  // Every buffer offset (Q, K and V loads, O stores) is 32-bit.
   int64_t pitch = d.q_ss > d.k_ss ? d.q_ss : d.k_ss;
   pitch = pitch > d.v_ss ? pitch : d.v_ss;
+  pitch = pitch > d.o_ss ? pitch : d.o_ss;
   const int64_t span = ((int64_t)d.S + kBQ) * 2 * pitch + 2 * d.D;
   if (span >= (1ll << 31)) return hipErrorNotSupported;
   int dev = 0, cus = 256;

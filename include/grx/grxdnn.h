@@ -127,7 +127,8 @@ grxdnnStatus_t grxdnnGeluForward(grxdnnHandle_t handle, grxdnnGeluMode_t mode,
  * [B, H, S, D] descriptors of one type (GRX_R_16BF or GRX_R_16F), innermost
  * stride 1, with equal B, H, S and D. Supported head dimensions: 64, 128.
  * The other strides are multiples of 8 elements and the pointers 16-byte
- * aligned (else NOT_SUPPORTED); O's elements must not share addresses (else
+ * aligned, and each tensor's sequence stride times 2 * (S + 256) bytes stays
+ * below 2^31 (else NOT_SUPPORTED); O's elements must not share addresses (else
  * INVALID_VALUE), while Q, K and V may (a broadcast). O must not overlap K
  * or V; it may be Q itself (same pointer, same strides: in place), and must
  * not overlap Q otherwise (else INVALID_VALUE, checked on the address ranges

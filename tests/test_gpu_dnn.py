@@ -352,6 +352,44 @@ def test_attention_strided_layout(dnn):
             assert normwise_rel_err(o[b, :, h], ref) <= 1e-2
 
 
+def test_attention_output_row_stride_and_span_limit(dnn):
+    """O rows far apart (128 KB sequence stride, heads back to back): every
+    row is right, and nothing else in the buffer is written -- not the gaps
+    between rows, not the rows past S of a query tile (S = 100: the last
+    tile's rows 100..127 would land on the next head's first rows), not the
+    guard rows after the last head. A stride whose 32-bit span check fails
+    is refused before any launch."""
+    B, H, S, D = 1, 2, 100, 128
+    o_ss = 1 << 16
+    r = np.random.default_rng(31)
+    shp = (B, H, S, D)
+    q, k, v = (O.f32_to_bf16(r.standard_normal(shp).astype(np.float32)) for _ in range(3))
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    total = (H * S + 32) * o_ss                       # 32 guard rows after the last head
+    sentinel = np.full(total, 0xFFFF, np.uint16)       # a bf16 NaN pattern
+    do = to_dev(sentinel)
+    din = g.TensorDesc(BF16, list(shp))
+    dout = g.TensorDesc(BF16, list(shp), [H * S * o_ss, S * o_ss, o_ss, 1])
+    ad = g.AttnDesc(True, D ** -0.5)
+    say("attention O sequence stride 2^16")
+    assert dnn.attention(ad, din, dq.p, din, dk.p, din, dv.p, dout, do.p) == g.SUCCESS
+    g.synchronize()
+    got = do.download(np.uint16, total)
+    rows = got[:H * S * o_ss].reshape(H, S, o_ss)
+    qf, kf, vf = (O.bf16_to_f32(a).reshape(shp) for a in (q, k, v))
+    for h in range(H):
+        ref = O.attention_head(qf[0, h], kf[0, h], vf[0, h], True, D ** -0.5)
+        assert normwise_rel_err(O.bf16_to_f32(rows[h, :, :D]), ref) <= 1e-2, h
+    assert (rows[:, :, D:] == 0xFFFF).all()
+    assert (got[H * S * o_ss:] == 0xFFFF).all()
+    # (S + 256) rows of 2 * o_ss bytes reach 2^31: NOT_SUPPORTED, O untouched
+    o_big = 3_100_000
+    big = g.DeviceBuffer(((S - 1) * o_big + D) * 2)
+    dbig = g.TensorDesc(BF16, [1, 1, S, D], [S * o_big, S * o_big, o_big, 1])
+    one = g.TensorDesc(BF16, [1, 1, S, D])
+    assert dnn.attention(ad, one, dq.p, one, dk.p, one, dv.p, dbig, big.p) == g.NOT_SUPPORTED
+
+
 def test_config5_full_size_sampled(dnn):
     """BASELINE config 5 at full size (B4 H32 S4096 D128 bf16, causal): all
     heads computed on the GPU; sampled heads and query rows (including the
