@@ -580,7 +580,12 @@ def main() -> int:
             w = loads.get(k)
             if w is not None and w.cpu is not None:
                 log(f"{w.name}: CPU baseline")
-                results[k]["cpu_baseline"] = w.cpu()
+                cb = w.cpu()
+                # the whole workload at the sampled rate (the sample is a slice)
+                scale = 1e9 if cb.get("unit") == "GB/s" else 1e12
+                if cb.get("value"):
+                    cb["full_problem_s_extrapolated"] = round(w.work / (cb["value"] * scale), 3)
+                results[k]["cpu_baseline"] = cb
     for w in loads.values():
         w.close()
     headline = results.get("gemm")
