@@ -59,3 +59,15 @@ def test_host_fields():
     d = bench.with_host({"value": 1.0})
     assert d["cpu_model"] and d["host_cpus"] >= 1
     assert 1 <= bench.cpu_threads() <= (os.cpu_count() or 1)
+
+
+@pytest.mark.parametrize("layer", [False, True])
+def test_norm_cpu_baseline_runs_every_row_it_is_given(layer):
+    from grxcp_amd import synth
+    rows, hidden = 64, 256
+    x = synth.normal_bf16(rows * hidden, 7)
+    g = synth.normal_bf16(hidden, 8, 1.0, 0.02)
+    b = synth.normal_bf16(hidden, 9, 0.0, 0.02)
+    d = bench.cpu_norm_baseline(x, g, b, rows, hidden, layer)
+    assert d["value"] > 0 and d["unit"] == "GB/s" and d["kind"] == "port"
+    assert d["sample"].startswith(f"{rows} of {rows} rows")
