@@ -223,8 +223,9 @@ def test_config4_full_size_sampled(dnn):
 
 # ---- attention -----------------------------------------------------------------
 
-def run_attention(dnn, t, B, H, S, D, causal, seed, q=None, k=None, v=None):
+def run_attention(dnn, t, B, H, S, D, causal, seed, q=None, k=None, v=None, scale=None):
     r = np.random.default_rng(seed)
+    scale = D ** -0.5 if scale is None else scale
     shp = (B, H, S, D)
     q = r.standard_normal(shp).astype(np.float32) if q is None else q
     k = r.standard_normal(shp).astype(np.float32) if k is None else k
@@ -233,8 +234,8 @@ def run_attention(dnn, t, B, H, S, D, causal, seed, q=None, k=None, v=None):
     dq, dk, dv = to_dev(qe), to_dev(ke), to_dev(ve)
     do = g.DeviceBuffer(qe.nbytes)
     desc = g.TensorDesc(t, list(shp))
-    ad = g.AttnDesc(causal, D ** -0.5)
-    say(f"attention t={t} B={B} H={H} S={S} D={D} causal={causal}")
+    ad = g.AttnDesc(causal, scale)
+    say(f"attention t={t} B={B} H={H} S={S} D={D} causal={causal} scale={scale:g}")
     s = dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p)
     assert s == g.SUCCESS, g.STATUS[s]
     g.synchronize()
@@ -271,6 +272,38 @@ def test_attention_closed_forms(dnn):
     vc = np.broadcast_to(r.standard_normal((B, H, 1, D)).astype(np.float32), (B, H, S, D)).copy()
     oc, _, _, vqc = run_attention(dnn, BF16, B, H, S, D, True, seed=5, v=vc)
     assert normwise_rel_err(oc, vqc) <= 1e-2
+
+
+@pytest.mark.parametrize("t", [BF16, F16])
+@pytest.mark.parametrize("case", ["growing", "huge_scale", "all_negative"])
+@pytest.mark.parametrize("D,causal", [(128, True), (64, False)])
+def test_attention_extreme_logits(dnn, t, case, D, causal):
+    """Logits the online softmax must rescale for: key magnitudes growing
+    along the sequence (each tile's maximum keeps overtaking the running one,
+    so the rescale of O and l runs again and again), a softmax scale of 20
+    (logits of a few hundred: exp overflows without the running-maximum
+    shift) and logits of about -4000 everywhere (exp underflows without it).
+    Every head against the float64 oracle, which shifts by the exact row
+    maximum."""
+    B, H, S = 1, 2, 300
+    r = np.random.default_rng({"growing": 61, "huge_scale": 62, "all_negative": 63}[case] + D)
+    shp = (B, H, S, D)
+    q, k, v = (r.standard_normal(shp).astype(np.float32) for _ in range(3))
+    scale = D ** -0.5
+    if case == "growing":
+        q *= 3.0
+        k *= (1.0 + 3.0 * np.arange(S, dtype=np.float32) / S)[None, None, :, None]
+    elif case == "huge_scale":
+        scale = 20.0
+    else:
+        q, k = np.abs(q), -np.abs(k)
+        scale = 50.0
+    o, qd, kd, vd = run_attention(dnn, t, B, H, S, D, causal, seed=0, q=q, k=k, v=v, scale=scale)
+    assert np.isfinite(o).all()
+    for b in range(B):
+        for h in range(H):
+            ref = O.attention_head(qd[b, h], kd[b, h], vd[b, h], causal, scale)
+            assert normwise_rel_err(o[b, h], ref) <= 1e-2, (case, b, h)
 
 
 @pytest.mark.parametrize("B,H,S,D,causal", [(4, 256, 64, 128, True), (4, 256, 64, 64, False),
