@@ -61,16 +61,40 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 
 // ---- reductions over one 64-wide wavefront ---------------------------------
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+// A butterfly that stays in the ALU: DPP moves within each row of 16 lanes
+// (quad permutes [1,0,3,2] and [2,3,0,1], then the half-row and row
+// mirrors, each pairing lanes whose partial results are disjoint), then
+// gfx950's row-swap instructions across rows of 16 and halves of 32. Every
+// lane ends with the same value (each step combines the same two partials
+// in every lane, and op is commutative). The shuffle form (__shfl_xor)
+// compiles to six dependent ds_bpermute LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  v = op(v, dpp_f<0xb1>(v));    // quad_perm [1,0,3,2]: lane ^ 1
+  v = op(v, dpp_f<0x4e>(v));    // quad_perm [2,3,0,1]: lane ^ 2
+  v = op(v, dpp_f<0x141>(v));   // row_half_mirror: the other quad of 8
+  v = op(v, dpp_f<0x140>(v));   // row_mirror: the other 8 of 16
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));   // the other row of 16
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));   // the other half of 32
+  }
   return v;
 }
 
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce(v, [](float a, float b) { return a + b; });
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // ---- cycle probe -------------------------------------------------------------
