@@ -337,3 +337,30 @@ def test_runtime_without_device():
     assert rt.grxMemcpy(FAKE, FAKE, 4, 7) == 6  # invalid direction, checked before HIP
     assert rt.grxStreamDestroy(None) == 7
     assert rt.grxEventRecord(None, None) == 7
+
+
+@pytest.mark.parametrize("lib", sorted(set(HEADERS.values())))
+def test_product_libraries_never_reach_the_oracle(lib):
+    """The oracle and the CPU host backend are test infrastructure: no
+    product library links them, names their symbols or loads them at run
+    time (no dlopen of a path containing them)."""
+    path = os.path.join(g.LIBDIR, lib)
+    dyn = subprocess.run(["readelf", "-d", path], capture_output=True, text=True, check=True).stdout
+    needed = re.findall(r"\(NEEDED\).*\[(.*)\]", dyn)
+    assert needed and not any("oracle" in n or "_ref" in n for n in needed), needed
+    undefined = subprocess.run(["nm", "-D", "--undefined-only", path], capture_output=True, text=True,
+                               check=True).stdout
+    assert "oracle_" not in undefined and "dlopen" not in undefined
+    strings = subprocess.run(["strings", path], capture_output=True, text=True, check=True).stdout
+    assert "libgrx_oracle" not in strings and "libgrxblas_ref" not in strings
+
+
+def test_product_python_never_imports_the_oracle():
+    """grxcp_amd's Python (the ctypes mirror the tests and bench.py use) has
+    no route to oracle/: no import of it and no path into it."""
+    pkg = os.path.join(ROOT, "grxcp_amd")
+    for name in os.listdir(pkg):
+        if name.endswith(".py"):
+            text = open(os.path.join(pkg, name)).read()
+            assert not re.search(r"^\s*(import|from)\s+oracle\b", text, re.M), name
+            assert "oracle/" not in text and "libgrx_oracle" not in text, name
