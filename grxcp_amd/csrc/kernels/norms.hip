@@ -7,15 +7,15 @@
 //
 //  * rows of up to 256 16-byte chunks (2048 bf16): one row per 64-lane
 //    wavefront, held packed in registers between the statistics pass and the
-//    output pass; both statistics are shuffle reductions, so there is no LDS
-//    and no barrier and every wave streams independently;
+//    output pass; both statistics are in-register wave reductions, so there
+//    is no LDS and no barrier and every wave streams independently;
 //  * longer rows (up to 4096 chunks): one row per workgroup of chunks/2
 //    threads (256, 512 or 1024), two chunks per thread held in registers,
 //    one LDS combine per statistic; x is still read from HBM exactly once;
 //  * longer still: x re-read per pass (from L2);
 //  * 16-byte non-temporal loads of x and stores of y, gamma/beta via the
 //    normal cached path (every row reuses them);
-//  * statistics in fp32: wavefront butterfly (__shfl_xor) then an LDS
+//  * statistics in fp32: wavefront butterfly (DPP and row swaps) then an LDS
 //    combine of the waves' partials, summed in a fixed order so every thread
 //    sees the same value.
 //    LayerNorm's variance is the two-pass (x - mean)^2 form over the cached
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(NT) void norm_block(NParams p) {
 
 // One row per 64-lane wavefront, for rows of up to NC x 64 16-byte chunks:
 // the row lives in the wave's registers, both statistics are wave
-// reductions (shuffles only: no LDS, no barrier), so every wave streams
+// reductions (lane moves only: no LDS, no barrier), so every wave streams
 // independently and a CU keeps ~20 rows of loads in flight.
 template <NormType T, bool LAYER, int NC>
 __global__ __launch_bounds__(256) void norm_wave(NParams p) {

@@ -5,8 +5,8 @@
 // neither. Both are HBM-bound streams: x is read once and y written once.
 //
 // Softmax, rows of up to 256 16-byte chunks: one row per wavefront, held
-// packed in registers; the row max and the sum of exp(x - max) are shuffle
-// reductions (no LDS, no barrier). Up to 4096 chunks: one row per workgroup,
+// packed in registers; the row max and the sum of exp(x - max) are in-register
+// wave reductions (no LDS, no barrier). Up to 4096 chunks: one row per workgroup,
 // two or four chunks per thread in registers, one LDS combine per statistic.
 // y = exp(x - max) / sum in fp32, rounded once (16-bit outputs use the
 // hardware exp2, fp32 the library expf). Longer or unaligned rows: one row
