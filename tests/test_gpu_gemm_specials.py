@@ -131,3 +131,62 @@ def test_sgemm_specials_and_subnormals(blas, capfd, name, m, n, k, kernel):
     assert np.max(np.abs(got[~special] - want[~special])) <= 1e-5 * (k + 1)
     for i, j in ((10, 11), (12, 13)):     # subnormal sums, kept exactly
         assert got[j * m + i] == want[j * m + i] != 0.0, (i, j, got[j * m + i], want[j * m + i])
+
+
+I8, I32 = g.GRX_R_8I, g.GRX_R_32I
+
+
+@pytest.mark.parametrize("alpha,beta", [(1, 0), (3, -2)])
+def test_int8_full_range_and_int32_wraparound(blas, capfd, alpha, beta):
+    """int8 operands over the whole range, -128 included, and a K long enough
+    that one accumulator passes 2^31: row 0 of A and column 0 of B all -128,
+    so C[0, 0] = 131328 * 16384 = 2151677952, which wraps to -2143289344
+    as in the oracle's (and C's) int32 arithmetic; alpha and beta also apply
+    in wrapping int32. Few tiles and a long K: the problem is split along K,
+    so the wrap passes through the partial sums and their reduction."""
+    m, n, k = 64, 96, 131328
+    r = np.random.default_rng(alpha + 7)
+    A = r.integers(-128, 128, (m, k)).astype(np.int8)     # ta=1: m rows of k
+    B = r.integers(-128, 128, (n, k)).astype(np.int8)     # tb=0: n columns of k
+    A[0, :] = -128
+    B[0, :] = -128
+    C = r.integers(-1000, 1000, m * n).astype(np.int32)
+    want = O.igemm(1, 0, m, n, k, alpha, A.ravel(), k, B.ravel(), k, beta, C, m)
+    exact = alpha * k * 16384 + beta * int(C[0])
+    assert exact > 2 ** 31 - 1 and int(want[0]) == (exact + 2 ** 31) % 2 ** 32 - 2 ** 31
+    dA, dB, dC = to_dev(A.ravel()), to_dev(B.ravel()), to_dev(C)
+    res = []
+
+    def call():
+        say(f"int8 wrap {m}x{n}x{k} alpha={alpha} beta={beta}")
+        res.append(blas.gemm_ex(1, 0, m, n, k, float(alpha), dA.p, I8, k, dB.p, I8, k, float(beta),
+                                dC.p, I32, m))
+        g.synchronize()
+    plans = logged_plans(capfd, call)
+    assert res == [g.SUCCESS], res
+    assert len(plans) == 1 and int(plans[0]["split"]) >= 2, plans
+    got = dC.download(np.int32, m * n)
+    assert np.array_equal(got, want), int(np.sum(got != want))
+
+
+def test_int8_dequant_of_a_wrapped_accumulator(blas):
+    """GemmExDequant takes the same wrapped int32 accumulator through
+    float(acc) * scale to bf16, bit-exact against the oracle."""
+    m, n, k = 64, 96, 131328
+    r = np.random.default_rng(11)
+    A = r.integers(-128, 128, (m, k)).astype(np.int8)
+    B = r.integers(-128, 128, (n, k)).astype(np.int8)
+    A[0, :] = -128
+    B[0, :] = -128
+    scale = r.uniform(0.001, 0.01, n).astype(np.float32)
+    acc = O.igemm(1, 0, m, n, k, 1, A.ravel(), k, B.ravel(), k, 0, np.zeros(m * n, np.int32), m)
+    want = O.dequant(m, n, acc, m, scale, m)
+    dA, dB, dS = to_dev(A.ravel()), to_dev(B.ravel()), to_dev(scale)
+    dC = to_dev(np.zeros(m * n, np.uint16))
+    say(f"dequant wrap {m}x{n}x{k}")
+    s = blas.gemm_ex_dequant(1, 0, m, n, k, dA.p, I8, k, dB.p, I8, k, dS.p, dC.p, BF16, m)
+    assert s == g.SUCCESS, g.STATUS[s]
+    g.synchronize()
+    got = dC.download(np.uint16, m * n)
+    assert np.array_equal(got, want), int(np.sum(got != want))
+    assert acc[0] < 0                                      # the wrapped value went through
