@@ -186,13 +186,16 @@ __global__ __launch_bounds__(256) void softmax_rows(RParams p) {
 }
 
 // The tanh form uses x/2 (1 + tanh z) = x * sigmoid(2z) = x / (1 + exp(-2z)):
-// one hardware exp2 and one reciprocal instead of a library tanh.
+// one hardware exp2 and one reciprocal instead of a library tanh. The erf
+// form uses 1 + erf(x/sqrt 2) = erfc(-x/sqrt 2). Neither cancels in the
+// negative tail (1 + erff(t) is 0 in fp32 from x = -5.4 on, and coarse
+// before it), so small results keep their relative precision.
 template <bool TANH> __device__ __forceinline__ float gelu(float x) {
   if (TANH) {
     const float z = 0.7978845608028654f * (x + 0.044715f * x * x * x);  // sqrt(2/pi)(x + 0.044715 x^3)
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * z));  // 2 log2(e)
   }
-  return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
+  return 0.5f * x * erfcf(x * -0.7071067811865476f);
 }
 
 template <NormType T, bool TANH>

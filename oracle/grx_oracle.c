@@ -307,6 +307,10 @@ void oracle_softmax(int rows, int hidden, int ld, const float* x, float* y) {
   }
 }
 
+/* GELU in forms without cancellation in the negative tail, where 1 + erf
+ * and 1 + tanh fall below double's resolution at 1 (x < -8.3, x < -6):
+ * 1/2 (1 + erf(x/sqrt 2)) = 1/2 erfc(-x/sqrt 2), and
+ * 1/2 (1 + tanh z) = 1 / (1 + exp(-2z)). Same values everywhere else. */
 void oracle_gelu(long n, int mode, const float* x, float* y) {
   /* mutation 8: erf(x) in place of erf(x / sqrt 2) */
   const double k = (g_mutation == 8) ? 1.0 : 1.0 / sqrt(2.0);
@@ -314,8 +318,12 @@ void oracle_gelu(long n, int mode, const float* x, float* y) {
   for (long i = 0; i < n; ++i) {
     const double v = (double)x[i];
     double g;
-    if (mode == 1) g = 0.5 * v * (1.0 + tanh(sqrt(2.0 / 3.14159265358979323846) * (v + 0.044715 * v * v * v)));
-    else g = 0.5 * v * (1.0 + erf(v * k));
+    if (mode == 1) {
+      const double z = sqrt(2.0 / 3.14159265358979323846) * (v + 0.044715 * v * v * v);
+      g = v / (1.0 + exp(-2.0 * z));
+    } else {
+      g = 0.5 * v * erfc(-v * k);
+    }
     y[i] = (float)g;
   }
 }

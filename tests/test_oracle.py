@@ -318,6 +318,31 @@ def test_gelu_published_values_identity_and_torch():
         np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-7)
 
 
+def test_gelu_far_tails_and_specials():
+    """The negative tail to relative precision, where 1 + erf and 1 + tanh
+    cancel in double (x < -8.3 and x < -6): against scipy's normal CDF
+    (x Phi(x), computed through erfc) and logistic (x expit(2z), the tanh
+    form's sigmoid), neither of which shares code with the oracle; and the
+    specials: gelu(+inf) = +inf, gelu(-inf) = NaN (-inf times 0, as the
+    formula gives), NaN stays NaN, far tails to +x and -0."""
+    import scipy.special as sp
+    x = np.concatenate([-np.geomspace(3.0, 40.0, 2000), np.geomspace(3.0, 40.0, 200)]).astype(np.float32)
+    xd = x.astype(np.float64)
+    z = np.sqrt(2.0 / np.pi) * (xd + 0.044715 * xd ** 3)
+    for mode, want in ((0, xd * sp.ndtr(xd)), (1, xd * sp.expit(2.0 * z))):
+        y = O.gelu(x, mode).astype(np.float64)
+        w = want.astype(np.float32).astype(np.float64)       # the oracle rounds once to fp32
+        normal = np.abs(w) >= np.finfo(np.float32).tiny
+        assert normal.sum() > 1000                          # down to x = -13 (erf), -10 (tanh)
+        np.testing.assert_allclose(y[normal], w[normal], rtol=2e-7, atol=0)
+        assert np.all(np.abs(y[~normal] - w[~normal]) <= 2.0 ** -149)
+    s = np.array([np.inf, -np.inf, np.nan, 1e30, -1e30], np.float32)
+    for mode in (0, 1):
+        y = O.gelu(s, mode)
+        assert y[0] == np.inf and np.isnan(y[1]) and np.isnan(y[2])
+        assert y[3] == np.float32(1e30) and y[4] == 0.0 and np.signbit(y[4])
+
+
 # ---- the checks above fail when a mistake is planted --------------------------
 
 @pytest.mark.parametrize("mutation,check", [
