@@ -185,17 +185,46 @@ __global__ __launch_bounds__(256) void softmax_rows(RParams p) {
   }
 }
 
+// Standard normal CDF, Phi(x) = erfc(-x / sqrt 2) / 2, through the Chebyshev
+// fit of erfc in Press et al., Numerical Recipes in C (2nd ed., section 6.2,
+// erfcc): erfc(z) = t exp(-z^2 + Q(t)), t = 1 / (1 + z/2), z >= 0, fractional
+// error below 1.2e-7 for every z (1.05e-7 measured in float64 against scipy).
+// The sign of x picks erfc(|z|)/2 or 1 - erfc(|z|)/2, so a small result is
+// never the difference of two numbers near 1 (1 + erff(x / sqrt 2) is 0 in
+// fp32 from x = -5.4 on), and no branch splits a wave. One reciprocal, one
+// exp2 and 14 other VALU instructions (16384 x 8192 bf16: 5980 GB/s, against
+// 5032 with the library erff and 3061 with the library erfcf, whose
+// interval branches make it compute-bound).
+__device__ __forceinline__ float normal_cdf(float x) {
+  const float z = fabsf(x) * 0.7071067811865476f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float q = 0.17087277f;
+  q = fmaf(t, q, -0.82215223f);
+  q = fmaf(t, q, 1.48851587f);
+  q = fmaf(t, q, -1.13520398f);
+  q = fmaf(t, q, 0.27886807f);
+  q = fmaf(t, q, -0.18628806f);
+  q = fmaf(t, q, 0.09678418f);
+  q = fmaf(t, q, 0.37409196f);
+  q = fmaf(t, q, 1.00002368f);
+  q = fmaf(t, q, -1.26551223f);
+  const float a = fmaf(-z, z, q);                          // ln(erfc(z) / t)
+  // erfc(z) / 2 = t * 2^(a log2(e) - 1)
+  const float h = t * __builtin_amdgcn_exp2f(fmaf(a, 1.4426950408889634f, -1.0f));
+  return x < 0.0f ? h : 1.0f - h;
+}
+
 // The tanh form uses x/2 (1 + tanh z) = x * sigmoid(2z) = x / (1 + exp(-2z)):
 // one hardware exp2 and one reciprocal instead of a library tanh. The erf
-// form uses 1 + erf(x/sqrt 2) = erfc(-x/sqrt 2). Neither cancels in the
-// negative tail (1 + erff(t) is 0 in fp32 from x = -5.4 on, and coarse
-// before it), so small results keep their relative precision.
+// form is x * Phi(x) with Phi as above. Neither forms 1 + erf or 1 + tanh,
+// which cancel in the negative tail, so small results keep their relative
+// precision.
 template <bool TANH> __device__ __forceinline__ float gelu(float x) {
   if (TANH) {
     const float z = 0.7978845608028654f * (x + 0.044715f * x * x * x);  // sqrt(2/pi)(x + 0.044715 x^3)
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * z));  // 2 log2(e)
   }
-  return 0.5f * x * erfcf(x * -0.7071067811865476f);
+  return x * normal_cdf(x);
 }
 
 template <NormType T, bool TANH>
