@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void softmax_rows(RParams p) {
 // The sign of x picks erfc(|z|)/2 or 1 - erfc(|z|)/2, so a small result is
 // never the difference of two numbers near 1 (1 + erff(x / sqrt 2) is 0 in
 // fp32 from x = -5.4 on), and no branch splits a wave. One reciprocal, one
-// exp2 and 14 other VALU instructions (16384 x 8192 bf16: 5980 GB/s, against
+// exp2 and 17 other VALU instructions (16384 x 8192 bf16: 5980 GB/s, against
 // 5032 with the library erff and 3061 with the library erfcf, whose
 // interval branches make it compute-bound).
 __device__ __forceinline__ float normal_cdf(float x) {
