@@ -536,6 +536,20 @@ def test_config2_bf16_sampled(blas, size):
     g.synchronize()
     C = O.bf16_to_f32(dC.download(np.uint16, M * N)).reshape(N, M)   # C[j, i] (column-major)
     assert np.isfinite(C).all()
+    # every column and every row through its sum: sum_i C[i, j] =
+    # (sum_i A[i, :]) . B[:, j] and sum_j C[i, j] = A[i, :] . (sum_j B[:, j]) in
+    # float64. The bf16 rounding of C (at most 2^-9 |C| per element,
+    # independent) moves a sum by ~2^-9 sqrt(sum C^2) / sqrt 3; allowed 8 times
+    # 2^-9 sqrt(sum C^2) (the exact product rounded to bf16 uses 0.37 of it at
+    # 2048^3), where a 256 x 256 tile holding another tile's values moves the
+    # sums through it by over 100 times the allowance.
+    af = O.bf16_to_f32(A).reshape(M, K)
+    bf = O.bf16_to_f32(B).reshape(N, K)
+    C64 = C.astype(np.float64)
+    for got, want, sq in ((C64.sum(1), bf @ af.sum(0, dtype=np.float64), (C64 * C64).sum(1)),
+                          (C64.sum(0), af @ bf.sum(0, dtype=np.float64), (C64 * C64).sum(0))):
+        assert np.all(np.abs(got - want) <= 8 * 2.0 ** -9 * np.sqrt(sq) + 1.0)
+    del af, bf, C64
     if size == 4096:
         af = O.bf16_to_f32(A).reshape(M, K).astype(np.float64)
         bf = O.bf16_to_f32(B).reshape(N, K).astype(np.float64)
@@ -577,6 +591,11 @@ def test_config3_int8_full_size(blas):
     colsum_a = A.reshape(M, K).sum(0, dtype=np.int64)
     rowsum_b = B.reshape(N, K).sum(0, dtype=np.int64)
     assert int(C.sum(dtype=np.int64)) == int(np.dot(colsum_a, rowsum_b))
+    # every column and every row, exactly: sum_i C[i, j] = (sum_i A[i, :]) . B[:, j]
+    # and sum_j C[i, j] = A[i, :] . (sum_j B[:, j]), so each 256 x 256 tile
+    # is pinned by the sums of the rows and columns through it
+    assert np.array_equal(C.sum(1, dtype=np.int64), B.reshape(N, K).astype(np.int64) @ colsum_a)
+    assert np.array_equal(C.sum(0, dtype=np.int64), A.reshape(M, K).astype(np.int64) @ rowsum_b)
     r = np.random.default_rng(1)
     rows = np.sort(np.concatenate([[0, 255, 256, M - 1], r.choice(M, 12, replace=False)]))
     cols = np.sort(np.concatenate([[0, 255, 256, N - 1], r.choice(N, 252, replace=False)]))
