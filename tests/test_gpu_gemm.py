@@ -576,8 +576,9 @@ def test_config3_int8_full_size(blas):
     """BASELINE config 3 at full size: M=4096 tokens, K=8192, N=28672; int8
     U[-127,127]. int32 C bit-exact on sampled rows x columns against the
     oracle, plus the whole-matrix checksum identity
-    sum_ij C = sum_l (sum_i A[i,l]) (sum_j B[l,j]); then the per-channel
-    dequant to bf16 bit-exact on the same samples."""
+    sum_ij C = sum_l (sum_i A[i,l]) (sum_j B[l,j]) and its every row and
+    column; then the per-channel dequant to bf16 bit-exact on the same
+    samples and over all outputs (the oracle's dequant of that int32 C)."""
     from grxcp_amd import synth
     M, K, N = 4096, 8192, 28672
     A = synth.uniform_int8(M * K, 31)   # row-major M x K  (transa=T, lda=K)
@@ -605,7 +606,6 @@ def test_config3_int8_full_size(blas):
     want = O.igemm(1, 0, m, n, K, 1, a.reshape(-1), K, b.reshape(-1), K, 0, np.zeros(m * n, np.int32),
                    m).reshape(n, m)
     assert np.array_equal(C[np.ix_(cols, rows)], want)
-    del C
     dC.close()
     dS, dY = to_dev(scale), g.DeviceBuffer(M * N * 2)
     say("config3 int8 dequant full size")
@@ -614,3 +614,8 @@ def test_config3_int8_full_size(blas):
     Y = dY.download(np.uint16, M * N).reshape(N, M)
     yw = O.dequant(m, n, want.reshape(-1), m, scale[cols], m).reshape(n, m)
     assert np.array_equal(Y[np.ix_(cols, rows)], yw)
+    # all 117 M bf16 outputs, bit for bit: the oracle's dequant of the int32
+    # result checked above (its sampled values exact, its row and column sums
+    # exact)
+    assert np.array_equal(Y, O.dequant(M, N, C.reshape(-1), M, scale, M).reshape(N, M))
+    del C
