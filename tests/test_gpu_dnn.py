@@ -195,10 +195,9 @@ def test_layernorm_constant_rows_give_beta_exactly(dnn):
     assert np.array_equal(y, np.tile(O.bf16_to_f32(O.f32_to_bf16(bq)), (rows, 1)))
 
 
-def test_config4_full_size_sampled(dnn):
-    """BASELINE config 4 at full size (16384 x 8192 bf16): every row computed on
-    the GPU, 64 sampled rows checked against the oracle element by element
-    (half a bf16 ulp plus fp32 arithmetic)."""
+def test_config4_full_size(dnn):
+    """BASELINE config 4 at full size (16384 x 8192 bf16): every row against
+    the oracle element by element (half a bf16 ulp plus fp32 arithmetic)."""
     from grxcp_amd import synth
     rows, hidden = 16384, 8192
     xb = synth.normal_bf16(rows * hidden, 41).reshape(rows, hidden)
@@ -206,7 +205,6 @@ def test_config4_full_size_sampled(dnn):
     bb = synth.normal_bf16(hidden, 43, 0.0, 0.02)
     dx, dg, db, dy = to_dev(xb), to_dev(gb), to_dev(bb), g.DeviceBuffer(rows * hidden * 2)
     xd, wd = g.TensorDesc(BF16, [rows, hidden]), g.TensorDesc(BF16, [hidden])
-    pick = np.random.default_rng(0).choice(rows, 64, replace=False)
     for layer in (False, True):
         say(f"config4 {'layernorm' if layer else 'rmsnorm'} full size")
         s = (dnn.layernorm(xd, dx.p, wd, dg.p, db.p, 1e-6, xd, dy.p) if layer
@@ -214,11 +212,13 @@ def test_config4_full_size_sampled(dnn):
         assert s == 0
         g.synchronize()
         y = dy.download(np.uint16, rows * hidden).reshape(rows, hidden)
-        xs = O.bf16_to_f32(xb[pick])
+        xs = O.bf16_to_f32(xb)
         gf, bf = O.bf16_to_f32(gb), O.bf16_to_f32(bb)
         ref = O.layernorm(xs, gf, bf, 1e-6) if layer else O.rmsnorm(xs, gf, 1e-6)
-        check_norm(O.bf16_to_f32(y[pick]), ref, bf if layer else None, BF16)
         yf = O.bf16_to_f32(y)
+        for r0 in range(0, rows, 2048):      # in slices, to bound host memory
+            check_norm(yf[r0:r0 + 2048], ref[r0:r0 + 2048], bf if layer else None, BF16)
+        del xs, ref
         assert np.isfinite(yf).all()
         # every row, size-independent: (y - beta) / gamma has mean square
         # ms / (ms + eps) = 1 - O(1e-6) on these rows, and mean 0 for LayerNorm,
@@ -432,10 +432,10 @@ def test_attention_output_row_stride_and_span_limit(dnn):
     assert dnn.attention(ad, one, dq.p, one, dk.p, one, dv.p, dbig, big.p) == g.NOT_SUPPORTED
 
 
-def test_config5_full_size_sampled(dnn):
-    """BASELINE config 5 at full size (B4 H32 S4096 D128 bf16, causal): all
-    heads computed on the GPU; sampled heads and query rows (including the
-    first and last of tiles and the sequence) checked against the oracle."""
+def test_config5_full_size(dnn):
+    """BASELINE config 5 at full size (B4 H32 S4096 D128 bf16, causal): every
+    query row of every head against the oracle (relative error of the row
+    <= 1e-2), plus size-independent properties."""
     from grxcp_amd import synth
     B, H, S, D = 4, 32, 4096, 128
     n = B * H * S * D
@@ -447,15 +447,18 @@ def test_config5_full_size_sampled(dnn):
     assert dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p) == 0
     g.synchronize()
     o = do.download(np.uint16, n).reshape(B, H, S, D)
-    rows = [0, 1, 63, 64, 127, 128, 129, 1000, 2047, 2048, 4094, 4095]
-    for (b, h) in [(0, 0), (1, 17), (3, 31)]:
-        q = O.bf16_to_f32(qb.reshape(B, H, S, D)[b, h])
-        k = O.bf16_to_f32(kb.reshape(B, H, S, D)[b, h])
-        v = O.bf16_to_f32(vb.reshape(B, H, S, D)[b, h])
-        for r0 in rows:
-            ref = O.attention_head(q, k, v, True, D ** -0.5, r0, r0 + 1)[r0]
-            got = O.bf16_to_f32(o[b, h, r0])
-            assert normwise_rel_err(got, ref) <= 1e-2, (b, h, r0)
+    worst = 0.0
+    for b in range(B):
+        for h in range(H):
+            q = O.bf16_to_f32(qb.reshape(B, H, S, D)[b, h])
+            k = O.bf16_to_f32(kb.reshape(B, H, S, D)[b, h])
+            v = O.bf16_to_f32(vb.reshape(B, H, S, D)[b, h])
+            ref = O.attention_head(q, k, v, True, D ** -0.5).astype(np.float64)
+            got = O.bf16_to_f32(o[b, h]).astype(np.float64)
+            rel = np.linalg.norm(got - ref, axis=1) / np.linalg.norm(ref, axis=1)
+            worst = max(worst, float(rel.max()))
+            assert rel.max() <= 1e-2, (b, h, int(rel.argmax()), float(rel.max()))
+    say(f"config5 worst row relative error {worst:.2e}")
     of = O.bf16_to_f32(o)
     assert np.isfinite(of).all()
     # every head, size-independent: row 0 attends to key 0 alone (O = V[0],

@@ -519,13 +519,14 @@ def test_bf16_random_normal_tolerance(blas):
 
 
 @pytest.mark.parametrize("size", [8192, 4096])
-def test_config2_bf16_sampled(blas, size):
+def test_config2_bf16_full(blas, size):
     """BASELINE config 2 at both of its sizes: bf16 8192^3 and 4096^3, TN
     (row-major A x column-major B), bf16 C. Sampled rows x columns against the
     fp64 oracle on the same bf16 inputs, max relative error <= 1e-2; every
-    output finite. At 4096^3 the whole matrix is also checked against numpy's
-    float64 product (an independent BLAS), normwise <= 1e-2 and per element
-    within bf16 rounding of the exact value plus the fp32 accumulation error."""
+    output finite. At both sizes the whole matrix is also checked against
+    numpy's float64 product (an independent BLAS), normwise <= 1e-2 and per
+    element within bf16 rounding of the exact value plus the fp32 accumulation
+    error."""
     from grxcp_amd import synth
     M = N = K = size
     A = synth.normal_bf16(M * K, 21)   # op(A): row-major M x K  (grxBLAS: transa=T, lda=K)
@@ -536,30 +537,15 @@ def test_config2_bf16_sampled(blas, size):
     g.synchronize()
     C = O.bf16_to_f32(dC.download(np.uint16, M * N)).reshape(N, M)   # C[j, i] (column-major)
     assert np.isfinite(C).all()
-    # every column and every row through its sum: sum_i C[i, j] =
-    # (sum_i A[i, :]) . B[:, j] and sum_j C[i, j] = A[i, :] . (sum_j B[:, j]) in
-    # float64. The bf16 rounding of C (at most 2^-9 |C| per element,
-    # independent) moves a sum by ~2^-9 sqrt(sum C^2) / sqrt 3; allowed 8 times
-    # 2^-9 sqrt(sum C^2) (the exact product rounded to bf16 uses 0.37 of it at
-    # 2048^3), where a 256 x 256 tile holding another tile's values moves the
-    # sums through it by over 100 times the allowance.
-    af = O.bf16_to_f32(A).reshape(M, K)
-    bf = O.bf16_to_f32(B).reshape(N, K)
-    C64 = C.astype(np.float64)
-    for got, want, sq in ((C64.sum(1), bf @ af.sum(0, dtype=np.float64), (C64 * C64).sum(1)),
-                          (C64.sum(0), af @ bf.sum(0, dtype=np.float64), (C64 * C64).sum(0))):
-        assert np.all(np.abs(got - want) <= 8 * 2.0 ** -9 * np.sqrt(sq) + 1.0)
-    del af, bf, C64
-    if size == 4096:
-        af = O.bf16_to_f32(A).reshape(M, K).astype(np.float64)
-        bf = O.bf16_to_f32(B).reshape(N, K).astype(np.float64)
-        full = bf @ af.T                                   # [j, i] like C
-        assert normwise_rel_err(C, full) <= 1e-2
-        # bf16 output: half an ulp (2^-9 relative) of rounding, plus fp32
-        # accumulation over K terms of magnitude |a||b| (~K * 2^-24 * sum|ab|)
-        bound = 2.0 ** -8 * np.abs(full) + K * 2.0 ** -23 * (np.abs(bf) @ np.abs(af).T)
-        assert np.all(np.abs(C - full) <= bound)
-        del af, bf, full, bound
+    af = O.bf16_to_f32(A).reshape(M, K).astype(np.float64)
+    bf = O.bf16_to_f32(B).reshape(N, K).astype(np.float64)
+    full = bf @ af.T                                   # [j, i] like C
+    assert normwise_rel_err(C, full) <= 1e-2
+    # bf16 output: half an ulp (2^-9 relative) of rounding, plus fp32
+    # accumulation over K terms of magnitude |a||b| (~K * 2^-24 * sum|ab|)
+    bound = 2.0 ** -8 * np.abs(full) + K * 2.0 ** -23 * (np.abs(bf) @ np.abs(af).T)
+    assert np.all(np.abs(C - full) <= bound)
+    del af, bf, full, bound
     r = np.random.default_rng(0)
     rows = np.sort(np.concatenate([[0, 255, 256, M - 1], r.choice(M, 12, replace=False)]))
     cols = np.sort(np.concatenate([[0, 255, 256, N - 1], r.choice(N, 124, replace=False)]))
@@ -577,8 +563,9 @@ def test_config3_int8_full_size(blas):
     U[-127,127]. int32 C bit-exact on sampled rows x columns against the
     oracle, plus the whole-matrix checksum identity
     sum_ij C = sum_l (sum_i A[i,l]) (sum_j B[l,j]) and its every row and
-    column; then the per-channel dequant to bf16 bit-exact on the same
-    samples and over all outputs (the oracle's dequant of that int32 C)."""
+    column, and all outputs against float64 BLAS (exact here); then the
+    per-channel dequant to bf16 bit-exact on the same samples and over all
+    outputs (the oracle's dequant of that int32 C)."""
     from grxcp_amd import synth
     M, K, N = 4096, 8192, 28672
     A = synth.uniform_int8(M * K, 31)   # row-major M x K  (transa=T, lda=K)
@@ -597,6 +584,12 @@ def test_config3_int8_full_size(blas):
     # is pinned by the sums of the rows and columns through it
     assert np.array_equal(C.sum(1, dtype=np.int64), B.reshape(N, K).astype(np.int64) @ colsum_a)
     assert np.array_equal(C.sum(0, dtype=np.int64), A.reshape(M, K).astype(np.int64) @ rowsum_b)
+    # and all 117 M outputs bit for bit against float64 BLAS: every product
+    # (|p| <= 127^2) and every partial sum (|s| < 2^27) is an integer that
+    # float64 holds exactly, so the float64 product is the exact int32 result
+    full = B.reshape(N, K).astype(np.float64) @ A.reshape(M, K).astype(np.float64).T   # [j, i] like C
+    assert np.array_equal(C, full.astype(np.int32))
+    del full
     r = np.random.default_rng(1)
     rows = np.sort(np.concatenate([[0, 255, 256, M - 1], r.choice(M, 12, replace=False)]))
     cols = np.sort(np.concatenate([[0, 255, 256, N - 1], r.choice(N, 252, replace=False)]))
