@@ -505,11 +505,20 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
   auto phase = [&](int buf, auto rd_st, int rd_ks, int dma_kt, int dma_st, int d0, int cnt, auto full) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const int i = q >> 1, j0 = 2 * (q & 1);
+      // int8: snake order (B reversed on odd A rows, so consecutive MFMAs
+      // never change both operands; +0.5 % on config-3 int8, same run, both
+      // library orders). The 16-bit types keep the plain order (snake: bf16
+      // 8192^3 +-0.1 %, 4096^3 -0.5 ... -2.5 %). Each accumulator's k order,
+      // and so every result, is the same either way.
+      constexpr bool kSnake = std::is_same<Op, OpI8>::value;
+      const int i = q >> 1;
+      const bool rev = kSnake && (i & 1) != 0;
+      const int ja = rev ? 3 - 2 * (q & 1) : 2 * (q & 1);
+      const int jb = rev ? ja - 1 : ja + 1;
       if ((q + 1) * cnt / 8 > q * cnt / 8) dma_d(dma_kt, dma_st, d0 + q * cnt / 8, full);
       __builtin_amdgcn_sched_barrier(0);
-      acc[i][j0] = Op::mma(fa[buf][i], fb[buf][j0], acc[i][j0]);
-      acc[i][j0 + 1] = Op::mma(fa[buf][i], fb[buf][j0 + 1], acc[i][j0 + 1]);
+      acc[i][ja] = Op::mma(fa[buf][i], fb[buf][ja], acc[i][ja]);
+      acc[i][jb] = Op::mma(fa[buf][i], fb[buf][jb], acc[i][jb]);
       frag(rd_st, rd_ks, buf ^ 1, q);
       __builtin_amdgcn_sched_barrier(0);
     }
