@@ -12,7 +12,7 @@ in the same places:
   entry takes all the weight;
 - GELU: gelu(+inf) = +inf, gelu(-inf) = NaN (-inf * 0, as the formula
   gives), NaN stays NaN, and the negative tail keeps its relative precision
-  down to the smallest normal output (1 + erf and 1 + tanh are not formed);
+  down to outputs of 2^-120 (1 + erf and 1 + tanh are not formed);
 - attention: a NaN in Q row i makes O row i NaN; a NaN in K row j makes the
   rows that attend to key j NaN and leaves the others (masked keys are
   replaced by -inf, not added to); a +inf key score makes its row NaN, a
