@@ -44,7 +44,8 @@ EXTRA = {
 
 LIBS = {
     "libgrxrt.so": (["runtime.cpp"], []),
-    "libgrxblas.so": (["grxblas.cpp", "kernels/gemm_mfma.hip", "kernels/sgemm.hip"], ["grxrt"]),
+    "libgrxblas.so": (["grxblas.cpp", "kernels/gemm_mfma.hip", "kernels/sgemm.hip",
+                       "kernels/noalloc_scratch.hip"], ["grxrt"]),
     "libgrxdnn.so": (["grxdnn.cpp", "kernels/norms.hip", "kernels/softmax_gelu.hip",
                       "kernels/attention.hip"], ["grxrt"]),
 }

@@ -234,9 +234,11 @@ grxblasStatus_t launch_gemm(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut ou
 }
 
 // The allocation-free form: the same plan with the library's static
-// per-device scratch (grxk::gemm_noalloc_scratch) in place of the handle's
+// per-device scratch (grxk::NoAllocScratch) in place of the handle's
 // workspace. Calls no hipMalloc/hipFree; a plan that needs more scratch
-// than the array holds is refused before anything is launched.
+// than the array holds is refused before anything is launched. A plan that
+// uses the scratch holds the device's scratch lock from before its launch
+// until the launch is recorded, so calls on other streams wait for it.
 grxblasStatus_t launch_gemm_noalloc(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut out,
                                     grxk::GemmDesc& d) {
   const size_t need = grxk::gemm_workspace_bytes(in, out, d);
@@ -248,13 +250,14 @@ grxblasStatus_t launch_gemm_noalloc(grxblasContext& ctx, grxk::MmaIn in, grxk::M
                  need, grxk::kNoAllocScratchBytes);
     return GRXBLAS_STATUS_NOT_SUPPORTED;
   }
-  if (need > 0) {
-    void* ws = grxk::gemm_noalloc_scratch();
-    if (!ws) return GRXBLAS_STATUS_INTERNAL_ERROR;
-    d.ws = ws;
-    d.ws_bytes = grxk::kNoAllocScratchBytes;
-  }
-  return from_hip(grxk::launch_mma_gemm(in, out, d, ctx.stream));
+  if (need == 0) return from_hip(grxk::launch_mma_gemm(in, out, d, ctx.stream));
+  grxk::NoAllocScratch scratch(ctx.stream);
+  if (!scratch.ptr()) return GRXBLAS_STATUS_INTERNAL_ERROR;
+  d.ws = scratch.ptr();
+  d.ws_bytes = grxk::kNoAllocScratchBytes;
+  const hipError_t e = grxk::launch_mma_gemm(in, out, d, ctx.stream);
+  const hipError_t r = scratch.release(e == hipSuccess);
+  return from_hip(e != hipSuccess ? e : r);
 }
 
 // GemmEx and its strided batch. Validation order of ref

@@ -36,7 +36,6 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
-#include <mutex>
 #include <type_traits>
 
 namespace grxk {
@@ -1376,39 +1375,6 @@ bool fp32_mma_wanted(const GemmDesc& d) {
   const int64_t waves = (units + 255) / 256;
   const int64_t last = units - (waves - 1) * 256;
   return units >= 256 && (waves >= 4 || last >= 192);
-}
-
-// ---- scratch of the allocation-free GemmEx entry point ---------------------
-//
-// grxblasGemmExNoAlloc runs the same plans as grxblasGemmEx, with the
-// transposed operand copies and split-K partials in this file-scope array
-// instead of a workspace the handle allocates. Each device that loads the
-// library holds its own copy (kNoAllocScratchBytes, zero-initialised storage
-// that is never written before a call uses it) until the process ends. In
-// host code `scratch` names a host-side stand-in, not device memory: its
-// device address comes from hipGetSymbolAddress, once per device, below.
-static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
-
-void* gemm_noalloc_scratch() {
-  constexpr int kMaxDevices = 64;
-  static std::mutex mu;
-  static void* addr[kMaxDevices] = {};
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  if (!addr[dev]) {
-    void* ptr = nullptr;
-    // resolved with `dev` current: each device's copy lives at its own address
-    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
-      (void)hipGetLastError();
-      return nullptr;
-    }
-    addr[dev] = ptr;
-  }
-  return addr[dev];
 }
 
 }  // namespace grxk

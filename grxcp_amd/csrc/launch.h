@@ -43,11 +43,28 @@ hipError_t launch_mma_gemm(MmaIn in, MmaOut out, const GemmDesc& d, hipStream_t 
 // Workspace bytes launch_mma_gemm would use for d (0: it needs none). With a
 // smaller d.ws_bytes the call takes the general path instead.
 size_t gemm_workspace_bytes(MmaIn in, MmaOut out, const GemmDesc& d);
-// Device address of the current device's scratch for grxblasGemmExNoAlloc
-// (kNoAllocScratchBytes, resolved once per device); null if it cannot be
-// resolved. Calls that overlap on one device share it, and race.
+// The current device's scratch for grxblasGemmExNoAlloc (kNoAllocScratchBytes,
+// a __device__ array in its own code object, resolved once per device) for
+// one launch on stream s. The constructor takes the device's lock and makes
+// s wait for the array's previous user on another stream; release(true)
+// records the launch behind it and drops the lock. ptr() is null if the
+// array cannot be resolved. Allocates nothing after the device's first call.
 constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
-void* gemm_noalloc_scratch();
+class NoAllocScratch {
+ public:
+  explicit NoAllocScratch(hipStream_t s);
+  ~NoAllocScratch();
+  NoAllocScratch(const NoAllocScratch&) = delete;
+  NoAllocScratch& operator=(const NoAllocScratch&) = delete;
+  void* ptr() const { return ptr_; }
+  hipError_t release(bool launched);
+
+ private:
+  hipStream_t stream_;
+  int dev_ = -1;
+  void* ptr_ = nullptr;
+  bool captured_ = false;
+};
 // fp32 problem d (MmaIn::F32 -> MmaOut::F32, no probe) that fills the GPU
 // with 256x256 tiles and can run the TN kernel, directly or behind copies.
 bool fp32_mma_wanted(const GemmDesc& d);

@@ -114,12 +114,17 @@ grxblasStatus_t grxblasGemmStridedBatchedEx(grxblasHandle_t handle,
  * arguments, type triples, validation, status codes and results as
  * grxblasGemmEx; where grxblasGemmEx would place transposed operand copies
  * or split-K partials in a workspace the handle allocates, this call uses a
- * static array of 64 MiB per device that the library holds until the
- * process ends (resolved on the first call on each device). A problem that
- * needs more scratch than that returns GRXBLAS_STATUS_NOT_SUPPORTED (with a
- * one-line message) and launches nothing. Every call on one device shares
- * that device's array: calls that overlap on one device (several streams or
- * threads at once) race and give wrong results. */
+ * static __device__ array of 64 MiB per device. The array is loaded onto a
+ * device by the first call of this function there (which also creates one
+ * event per device; make that first call outside graph capture), and the
+ * device then holds it until the process ends; processes that never call
+ * this function do not hold it. A problem that needs more scratch than that
+ * returns GRXBLAS_STATUS_NOT_SUPPORTED (with a one-line message) and
+ * launches nothing. Every call on one device shares that device's array:
+ * a call on another stream than the previous scratch user's waits, on the
+ * GPU, for that user's launch (hipStreamWaitEvent), so calls from several
+ * streams, handles or threads take turns. Under HIP graph capture that wait
+ * is left out: a captured call is ordered only by its graph and stream. */
 grxblasStatus_t grxblasGemmExNoAlloc(grxblasHandle_t handle,
                                      grxblasOperation_t transa,
                                      grxblasOperation_t transb,
