@@ -143,6 +143,8 @@ _DNN = {
     "grxdnnGetAttentionDescriptor": (c_int, [c_void_p, _IP, _FP]),
     "grxdnnAttentionForward": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "grxdnnSetCycleProbe": (c_int, [c_void_p, c_void_p, c_int]),
+    "grxdnnAttentionCycleSlotsNeeded": (c_int, [c_void_p, c_int, c_int, c_int]),
 }
 EXPORTS = {"libgrxrt.so": _RT, "libgrxblas.so": _BLAS, "libgrxdnn.so": _DNN}
 
@@ -368,6 +370,14 @@ class Dnn:
 
     def attention(self, ad, qd, q, kd, k, vd, v, od, o) -> int:
         return self.L.grxdnnAttentionForward(self.h, ad.d, qd.d, q, kd.d, k, vd.d, v, od.d, o)
+
+    def set_cycle_probe(self, slots, capacity: int) -> int:
+        """Attach (or with slots=None detach) a device array of CycleSlot
+        for the attention calls."""
+        return self.L.grxdnnSetCycleProbe(self.h, slots, capacity)
+
+    def attention_cycle_slots_needed(self, batch: int, heads: int, seq: int) -> int:
+        return self.L.grxdnnAttentionCycleSlotsNeeded(self.h, batch, heads, seq)
 
     def softmax(self, xd, x, yd, y) -> int:
         return self.L.grxdnnSoftmaxForward(self.h, xd.d, x, yd.d, y)

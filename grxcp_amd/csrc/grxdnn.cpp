@@ -12,7 +12,9 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <array>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -24,6 +26,8 @@
 
 struct grxdnnContext {
   hipStream_t stream = nullptr;
+  grxCycleSlot* probe = nullptr;
+  int probe_capacity = 0;
   std::mutex mutex;
   std::array<signed char, 64> device_ok{};
   grxdnnStatus_t device_status[64];
@@ -154,6 +158,65 @@ bool same_strides(const grxdnnTensorStruct& a, const grxdnnTensorStruct& b) {
   for (int i = 0; i < a.nb; ++i)
     if (a.strides[i] != b.strides[i]) return false;
   return true;
+}
+
+// Whether delta = sum_i strides[i] * d_i has a solution with |d_i| <
+// extents[i], for dimensions taken in decreasing stride order from `from`;
+// reach[i] is the largest |sum| the dimensions after i can make. Returns
+// true ("may share an element") when the search would take too many steps.
+bool offset_reachable(const int64_t* strides, const int64_t* extents, const int64_t* reach,
+                      int n, int from, int64_t delta, int* budget) {
+  if (from == n) return delta == 0;
+  const int64_t s = strides[from], r = reach[from], e = extents[from] - 1;
+  // d with |delta - s*d| <= r: d in [ceil((delta-r)/s), floor((delta+r)/s)]
+  auto floor_div = [](int64_t a, int64_t b) { return a >= 0 ? a / b : -((-a + b - 1) / b); };
+  int64_t lo = -floor_div(-(delta - r), s), hi = floor_div(delta + r, s);
+  if (lo < -e) lo = -e;
+  if (hi > e) hi = e;
+  for (int64_t d = lo; d <= hi; ++d) {
+    if (--*budget < 0) return true;
+    if (offset_reachable(strides, extents, reach, n, from + 1, delta - s * d, budget)) return true;
+  }
+  return false;
+}
+
+// Two views of one shape and the same strides (bases a and b, elements of
+// `elem` bytes) share an element's address. An exact test of the element
+// offsets, so that e.g. O written over the Q slot of a packed [B,S,3,H,D]
+// QKV buffer is told apart from O overlapping K or V. Views whose bases do
+// not differ by whole elements are taken to overlap when their spans do.
+bool views_share_element(const grxdnnTensorStruct& t, const void* a, const void* b, size_t elem) {
+  const int64_t diff = (int64_t)((intptr_t)b - (intptr_t)a);
+  if (diff % (int64_t)elem != 0) return intersect(span_of(t, a, elem), span_of(t, b, elem));
+  int64_t strides[GRXDNN_DIM_MAX], extents[GRXDNN_DIM_MAX], reach[GRXDNN_DIM_MAX];
+  int n = 0;
+  for (int i = 0; i < t.nb; ++i) {
+    if (t.dims[i] <= 0) return false;                      // an empty view
+    if (t.dims[i] == 1 || t.strides[i] == 0) continue;     // contributes no offset
+    strides[n] = t.strides[i];
+    extents[n] = t.dims[i];
+    ++n;
+  }
+  for (int x = 1; x < n; ++x)                              // decreasing stride
+    for (int y = x; y > 0 && strides[y] > strides[y - 1]; --y) {
+      std::swap(strides[y], strides[y - 1]);
+      std::swap(extents[y], extents[y - 1]);
+    }
+  int64_t acc = 0;
+  for (int i = n - 1; i >= 0; --i) {
+    reach[i] = acc;
+    acc += strides[i] * (extents[i] - 1);
+  }
+  int budget = 4096;
+  return offset_reachable(strides, extents, reach, n, 0, diff / (int64_t)elem, &budget);
+}
+
+// O may share no element with x: the exact test where the two views have the
+// same strides, the span test otherwise.
+bool may_alias(const grxdnnTensorStruct& od, const void* o, const grxdnnTensorStruct& xd,
+               const void* x) {
+  if (same_strides(od, xd)) return views_share_element(od, o, x, 2);
+  return intersect(span_of(od, o, 2), span_of(xd, x, 2));
 }
 
 grxdnnStatus_t norm_common(grxdnnHandle_t handle, grxdnnTensorDescriptor_t xDesc, const void* x,
@@ -439,13 +502,14 @@ grxdnnStatus_t grxdnnAttentionForward(grxdnnHandle_t handle, grxdnnAttentionDesc
   if (!no_overlap(*oDesc)) return GRXDNN_STATUS_INVALID_VALUE;
   if (!q || !k || !v || !o) return GRXDNN_STATUS_INVALID_VALUE;
   // A workgroup writes its O rows while workgroups of other query tiles of
-  // the same head still read K and V, so O may not overlap them. O == Q with
-  // the same layout is safe (a workgroup reads only its own Q rows, before it
-  // writes them); any other overlap with Q is refused too.
-  const Span so = span_of(*oDesc, o, 2);
-  if (intersect(so, span_of(*kDesc, k, 2)) || intersect(so, span_of(*vDesc, v, 2)))
+  // the same head still read K and V, so O may not share an element with
+  // them. O == Q with the same layout is safe (a workgroup reads only its own
+  // Q rows, before it writes them); any other overlap with Q is refused too.
+  // Views with O's strides are compared element by element (O over the Q
+  // slot of a packed QKV buffer is accepted), others by their byte spans.
+  if (may_alias(*oDesc, o, *kDesc, k) || may_alias(*oDesc, o, *vDesc, v))
     return GRXDNN_STATUS_INVALID_VALUE;
-  if (intersect(so, span_of(*qDesc, q, 2)) && !(o == q && same_strides(*oDesc, *qDesc)))
+  if (may_alias(*oDesc, o, *qDesc, q) && !(o == q && same_strides(*oDesc, *qDesc)))
     return GRXDNN_STATUS_INVALID_VALUE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return GRXDNN_STATUS_NOT_SUPPORTED;
@@ -461,8 +525,32 @@ grxdnnStatus_t grxdnnAttentionForward(grxdnnHandle_t handle, grxdnnAttentionDesc
   d.k = k; d.k_sb = kDesc->strides[0]; d.k_sh = kDesc->strides[1]; d.k_ss = kDesc->strides[2];
   d.v = v; d.v_sb = vDesc->strides[0]; d.v_sh = vDesc->strides[1]; d.v_ss = vDesc->strides[2];
   d.o = o; d.o_sb = oDesc->strides[0]; d.o_sh = oDesc->strides[1]; d.o_ss = oDesc->strides[2];
+  {
+    std::lock_guard<std::mutex> lock(handle->mutex);
+    if (handle->probe) {
+      if (handle->probe_capacity < grxk::attention_probe_slots(B, H, S))
+        return GRXDNN_STATUS_INVALID_VALUE;
+      d.probe = handle->probe;
+    }
+  }
   return from_hip(grxk::launch_attention(
       t == GRX_R_16BF ? grxk::AttnType::BF16 : grxk::AttnType::F16, d, handle->stream));
+}
+
+grxdnnStatus_t grxdnnSetCycleProbe(grxdnnHandle_t handle, grxCycleSlot* slots, int capacity) {
+  if (!handle) return GRXDNN_STATUS_NOT_INITIALIZED;
+  if (slots && capacity <= 0) return GRXDNN_STATUS_INVALID_VALUE;
+  std::lock_guard<std::mutex> lock(handle->mutex);
+  handle->probe = slots;
+  handle->probe_capacity = slots ? capacity : 0;
+  return GRXDNN_STATUS_SUCCESS;
+}
+
+int grxdnnAttentionCycleSlotsNeeded(grxdnnHandle_t handle, int batch, int heads, int seqLen) {
+  (void)handle;
+  if (batch <= 0 || heads <= 0 || seqLen <= 0) return 0;
+  const int64_t s = grxk::attention_probe_slots(batch, heads, seqLen);
+  return s > INT_MAX ? INT_MAX : (int)s;
 }
 
 }  // extern "C"

@@ -147,6 +147,7 @@ struct AParams {
   int heads;      // B * H
   int causal;
   float c;  // scale * log2(e)
+  grxCycleSlot* probe;   // one slot per wave, or null
 };
 
 // K rows: ds_read_b128 of one logical chunk by 32 consecutive rows must hit
@@ -223,6 +224,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
   // D = 128; 160 KB of LDS in all).
   __shared__ __attribute__((aligned(1024))) i32x4 ost[kNW][32 * CH];
 
+  const uint64_t t_start = cycle_now();
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -526,6 +528,21 @@ __global__ __launch_bounds__(64 * kNW, 1) void attn_fwd(AParams p) {
     tile(Stage<2>{});
     if (done) break;
   }
+  cycle_record(p.probe, t_start, blockIdx.x * kNW + wave, wave);
+}
+
+// One workgroup per CU, a multiple of 8 (one share per XCD), no more than
+// the items need.
+int64_t workgroups(int B, int H, int S) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int64_t qtiles = (S + kBQ - 1) / kBQ;
+  int64_t wgs = (cus / 8) * 8;
+  const int64_t per_xcd_items = ((int64_t)B * H + 7) / 8 * qtiles;
+  if (wgs / 8 > per_xcd_items) wgs = 8 * per_xcd_items;
+  if (wgs < 8) wgs = 8;
+  return wgs;
 }
 
 template <AttnType T, int D>
@@ -542,28 +559,23 @@ hipError_t run(const AttnDesc& d, hipStream_t s) {
   p.heads = d.B * d.H;
   p.causal = d.causal ? 1 : 0;
   p.c = d.scale * 1.4426950408889634f;
+  p.probe = d.probe;
   // Every buffer offset (Q, K and V loads, O stores) is 32-bit.
   int64_t pitch = d.q_ss > d.k_ss ? d.q_ss : d.k_ss;
   pitch = pitch > d.v_ss ? pitch : d.v_ss;
   pitch = pitch > d.o_ss ? pitch : d.o_ss;
   const int64_t span = ((int64_t)d.S + kBQ) * 2 * pitch + 2 * d.D;
   if (span >= (1ll << 31)) return hipErrorNotSupported;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess)
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   // item indices are 32-bit in the kernel
   if ((int64_t)d.B * d.H * p.qtiles > 0x7fffffff) return hipErrorInvalidValue;
-  // one workgroup per CU, a multiple of 8 (one share per XCD), no more than
-  // the items need
-  int64_t wgs = (cus / 8) * 8;
-  const int64_t per_xcd_items = ((int64_t)(p.heads + 7) / 8) * p.qtiles;
-  if (wgs / 8 > per_xcd_items) wgs = 8 * per_xcd_items;
-  if (wgs < 8) wgs = 8;
+  const int64_t wgs = workgroups(d.B, d.H, d.S);
   hipLaunchKernelGGL((attn_fwd<T, D>), dim3((unsigned)wgs), dim3(64 * kNW), 0, s, p);
   return hipGetLastError();
 }
 
 }  // namespace
+
+int64_t attention_probe_slots(int B, int H, int S) { return workgroups(B, H, S) * kNW; }
 
 hipError_t launch_attention(AttnType t, const AttnDesc& d, hipStream_t s) {
   if (t == AttnType::BF16) {

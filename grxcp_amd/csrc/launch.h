@@ -126,8 +126,12 @@ struct AttnDesc {
   const void* k; int64_t k_sb, k_sh, k_ss;
   const void* v; int64_t v_sb, v_sh, v_ss;
   void* o;       int64_t o_sb, o_sh, o_ss;
+  grxCycleSlot* probe = nullptr;   // one slot per wave of the launch, or null
 };
 hipError_t launch_attention(AttnType t, const AttnDesc& d, hipStream_t s);
+// Probe slots an attention launch of this shape uses on the current device
+// (workgroups x waves per workgroup; slot = blockIdx * waves + wave).
+int64_t attention_probe_slots(int B, int H, int S);
 
 }  // namespace grxk
 

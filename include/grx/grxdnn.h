@@ -16,6 +16,7 @@
 #ifndef GRXDNN_H
 #define GRXDNN_H
 
+#include "grx_cycles.h"
 #include "grx_runtime.h"
 #include "grx_types.h"
 
@@ -129,10 +130,12 @@ grxdnnStatus_t grxdnnGeluForward(grxdnnHandle_t handle, grxdnnGeluMode_t mode,
  * The other strides are multiples of 8 elements and the pointers 16-byte
  * aligned, and each tensor's sequence stride times 2 * (S + 256) bytes stays
  * below 2^31 (else NOT_SUPPORTED); O's elements must not share addresses (else
- * INVALID_VALUE), while Q, K and V may (a broadcast). O must not overlap K
- * or V; it may be Q itself (same pointer, same strides: in place), and must
- * not overlap Q otherwise (else INVALID_VALUE, checked on the address ranges
- * the descriptors span).
+ * INVALID_VALUE), while Q, K and V may (a broadcast). O must share no
+ * element with K or V, and none with Q unless it is Q itself (same pointer,
+ * same strides: in place); else INVALID_VALUE. Where O and the other view
+ * have the same strides the test is exact, element by element (O in its own
+ * slot of a packed [B, S, n, H, D] buffer is accepted); otherwise it is on
+ * the address ranges the descriptors span.
  * Softmax and both products accumulate in fp32; O is rounded once (RNE). */
 grxdnnStatus_t grxdnnCreateAttentionDescriptor (grxdnnAttentionDescriptor_t* d);
 grxdnnStatus_t grxdnnDestroyAttentionDescriptor(grxdnnAttentionDescriptor_t d);
@@ -148,6 +151,19 @@ grxdnnStatus_t grxdnnAttentionForward(grxdnnHandle_t handle,
                                       grxdnnTensorDescriptor_t kDesc, const void* k,
                                       grxdnnTensorDescriptor_t vDesc, const void* v,
                                       grxdnnTensorDescriptor_t oDesc, void* o);
+
+/* Per-wave cycle records of grxdnnAttentionForward, in grxBLAS's probe
+ * format and manner (grx_cycles.h; ref include/grx/grxblas.h:240-242, which
+ * grxDNN, new, extends to attention). With a slot array attached, the next
+ * attention calls write one grxCycleSlot per wave that has work (slot =
+ * workgroup * waves per workgroup + wave; s_memtime at entry and exit, core
+ * = XCD << 16 | CU id); capacity must cover
+ * grxdnnAttentionCycleSlotsNeeded for the call's B, H and S, else the call
+ * returns INVALID_VALUE before any device work. NULL turns recording off. */
+grxdnnStatus_t grxdnnSetCycleProbe(grxdnnHandle_t handle, grxCycleSlot* slots,
+                                   int capacity);
+int            grxdnnAttentionCycleSlotsNeeded(grxdnnHandle_t handle, int batch,
+                                               int heads, int seqLen);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -232,6 +232,25 @@ def test_attention_broadcast_input_passes_validation():
     assert D.grxdnnDestroy(h) == g.SUCCESS
 
 
+def test_dnn_cycle_probe_arguments():
+    """grxdnnSetCycleProbe follows grxblasSetCycleProbe's argument rules; the
+    slot count is workgroups x 8 waves (here the 256-CU default of a host
+    without a device: at most one workgroup per CU, a multiple of 8, no more
+    than the (batch, head, 256-query) items of the busiest XCD need)."""
+    D = g.load().dnn
+    h = ctypes.c_void_p()
+    assert D.grxdnnCreate(ctypes.byref(h)) == g.SUCCESS
+    assert D.grxdnnSetCycleProbe(h, ctypes.c_void_p(8), 0) == g.INVALID_VALUE
+    assert D.grxdnnSetCycleProbe(h, ctypes.c_void_p(8), 64) == g.SUCCESS
+    assert D.grxdnnSetCycleProbe(h, None, 0) == g.SUCCESS
+    assert D.grxdnnSetCycleProbe(None, None, 0) == g.NOT_INITIALIZED
+    assert D.grxdnnAttentionCycleSlotsNeeded(h, 1, 1, 1) == 8 * 8
+    assert D.grxdnnAttentionCycleSlotsNeeded(h, 2, 8, 512) == 8 * 4 * 8   # 2 heads x 2 tiles per XCD
+    assert D.grxdnnAttentionCycleSlotsNeeded(h, 4, 32, 4096) == 256 * 8
+    assert D.grxdnnAttentionCycleSlotsNeeded(h, 0, 32, 4096) == 0
+    assert D.grxdnnDestroy(h) == g.SUCCESS
+
+
 def test_attention_output_overlapping_k_or_v_is_refused():
     """A workgroup writes its O rows while workgroups of other query tiles of
     the same head still read K and V: an O that overlaps K or V (or overlaps
@@ -256,6 +275,25 @@ def test_attention_output_overlapping_k_or_v_is_refused():
     if ok is not None:
         assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, P(0x200000 + 8192)) == ok
         assert att(h, ad.d, q.d, fq, q.d, fk, q.d, fv, q.d, P(0x200000 - 8192)) == ok
+    # a packed [B, S, 3, H, D] QKV buffer: Q, K and V are views with one set
+    # of strides, 2*H*D bytes apart. O written over the Q slot shares no
+    # element with K or V (their spans interleave): accepted. O over the K
+    # slot, or shifted by one head or by 8 elements, shares elements: refused.
+    B_, H_, S_, D_ = 2, 2, 16, 128
+    qkv = g.TensorDesc(g.GRX_R_16BF, [B_, H_, S_, D_], [S_ * 3 * H_ * D_, D_, 3 * H_ * D_, 1])
+    base = 0x1000000
+    pq, pk, pv = P(base), P(base + 2 * H_ * D_), P(base + 4 * H_ * D_)
+    assert att(h, ad.d, qkv.d, pk, qkv.d, pk, qkv.d, pv, qkv.d, pk) == g.INVALID_VALUE   # O == K
+    assert att(h, ad.d, qkv.d, pq, qkv.d, pk, qkv.d, pv, qkv.d, P(base + 2 * D_)) == g.INVALID_VALUE
+    assert att(h, ad.d, qkv.d, pq, qkv.d, pk, qkv.d, pv, qkv.d,
+               P(base + 2 * H_ * D_ - 16)) == g.INVALID_VALUE
+    assert att(h, ad.d, qkv.d, pq, qkv.d, pk, qkv.d, pv, qkv.d,
+               P(base + 4 * H_ * D_ + 2 * D_)) == g.INVALID_VALUE                          # O over V's head 1
+    if ok is not None:
+        assert att(h, ad.d, qkv.d, pq, qkv.d, pk, qkv.d, pv, qkv.d, pq) == ok              # in place
+        # a separate contiguous O: fine
+        dense = g.TensorDesc(g.GRX_R_16BF, [B_, H_, S_, D_])
+        assert att(h, ad.d, qkv.d, pq, qkv.d, pk, qkv.d, pv, dense.d, P(0x4000000)) == ok
     assert D.grxdnnDestroy(h) == g.SUCCESS
 
 

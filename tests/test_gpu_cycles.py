@@ -157,3 +157,41 @@ def test_probe_level12(blas):
         out = dw.download(np.float32, nn if trans else m)
         assert np.all(out == (m if trans else nn))
         check_written(slots, range(4 * blocks))
+
+
+def test_probe_attention(dnn):
+    """grxdnnSetCycleProbe: one slot per attention wave that has work, at
+    workgroup * 8 + wave. One (batch, head) of 512 queries is two 256-query
+    items, both on the head's XCD share (workgroups 0 and 8 of 16: XCD
+    share = workgroup % 8); the other shares have no work and write nothing.
+    Workgroups 0 and 8 run on one hardware XCD, which the kernel's head split
+    assumes. With one slot too few the call is refused before any launch."""
+    import oracle as O
+    B, H, S, D = 1, 1, 512, 128
+    nslots = dnn.attention_cycle_slots_needed(B, H, S)
+    assert nslots == 16 * 8
+    r = np.random.default_rng(7)
+    q, k, v = (O.f32_to_bf16(r.standard_normal((S, D)).astype(np.float32)) for _ in range(3))
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    do = to_dev(np.full(S * D, 0x7FC0, np.uint16))
+    desc = g.TensorDesc(g.GRX_R_16BF, [B, H, S, D])
+    ad = g.AttnDesc(True, D ** -0.5)
+    call = lambda: dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, do.p)  # noqa: E731
+    say("probe attention, one slot short")
+    s, slots = probe_call(dnn, nslots - 1, call)
+    assert s == g.INVALID_VALUE and not np.any(slots["end"])
+    assert np.all(do.download(np.uint16, S * D) == 0x7FC0)
+    say("probe attention B=1 H=1 S=512 D=128 causal")
+    s, slots = probe_call(dnn, nslots, call)
+    assert s == g.SUCCESS, g.STATUS[s]
+    written = np.nonzero((slots["start"] != 0) | (slots["end"] != 0))[0]
+    assert written.tolist() == list(range(0, 8)) + list(range(64, 72))
+    w = slots[written]
+    assert np.all(w["end"] > w["start"]) and np.all(w["end"] - w["start"] < 10**9)
+    assert np.all(w["warp"] == written % 8)
+    assert len(set((w["core"] >> 16).tolist())) == 1, "workgroups 0 and 8 on one XCD"
+    assert len(set(w[:8]["core"].tolist())) == 1 and len(set(w[8:]["core"].tolist())) == 1
+    o = O.bf16_to_f32(do.download(np.uint16, S * D)).reshape(S, D)
+    ref = O.attention_head(O.bf16_to_f32(q).reshape(S, D), O.bf16_to_f32(k).reshape(S, D),
+                           O.bf16_to_f32(v).reshape(S, D), True, D ** -0.5)
+    assert np.max(np.abs(o - ref)) / np.max(np.abs(ref)) <= 1e-2

@@ -10,6 +10,8 @@ Attention: max relative error 1e-2 of the fp64 reference. Closed forms are
 checked exactly where the arithmetic is exact (LayerNorm of a constant row is
 beta; attention row 0 is V[0]).
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -327,6 +329,64 @@ def test_attention_many_items_per_workgroup(dnn, B, H, S, D, causal):
         for h in range(H):
             ref = O.attention_head(q[b, h], k[b, h], v[b, h], causal, D ** -0.5)
             assert normwise_rel_err(o[b, h], ref) <= 1e-2, (b, h)
+
+
+@pytest.mark.parametrize("B,H,S,D,causal", [(2, 3, 256, 128, True), (2, 3, 333, 64, False),
+                                             (4, 256, 64, 128, True), (4, 256, 64, 64, False),
+                                             (2, 128, 300, 128, True), (1, 64, 520, 128, False)])
+def test_attention_in_place(dnn, B, H, S, D, causal):
+    """O written over Q (the same buffer and descriptor): a workgroup loads
+    each item's Q before it stores that item's O, and the next item's Q rows
+    are other rows, so the result equals the out-of-place one. Shapes where
+    every persistent workgroup runs several items, causal and not, both head
+    dimensions, S beyond one query tile. Every head against the oracle
+    computed from the original Q."""
+    r = np.random.default_rng(B * H + S + D + 7)
+    shp = (B, H, S, D)
+    q, k, v = (O.f32_to_bf16(r.standard_normal(shp).astype(np.float32)) for _ in range(3))
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    desc = g.TensorDesc(BF16, list(shp))
+    ad = g.AttnDesc(causal, D ** -0.5)
+    say(f"attention in place B={B} H={H} S={S} D={D} causal={causal}")
+    assert dnn.attention(ad, desc, dq.p, desc, dk.p, desc, dv.p, desc, dq.p) == g.SUCCESS
+    g.synchronize()
+    o = O.bf16_to_f32(dq.download(np.uint16, q.size)).reshape(shp)
+    qf, kf, vf = (O.bf16_to_f32(a).reshape(shp) for a in (q, k, v))
+    assert np.array_equal(dk.download(np.uint16, k.size), k.ravel())
+    assert np.array_equal(dv.download(np.uint16, v.size), v.ravel())
+    for b in range(B):
+        for h in range(H):
+            ref = O.attention_head(qf[b, h], kf[b, h], vf[b, h], causal, D ** -0.5)
+            assert normwise_rel_err(o[b, h], ref) <= 1e-2, (b, h)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_packed_qkv_output_over_q(dnn, causal):
+    """A packed [B, S, 3, H, D] QKV buffer with O written over its Q slot
+    (O == Q, same strides): K and V, whose rows interleave with Q's, are left
+    as they were, and every head matches the oracle on the original Q."""
+    B, H, S, D = 2, 8, 384, 128
+    r = np.random.default_rng(17 + causal)
+    qkv = O.f32_to_bf16(r.standard_normal((B, S, 3, H, D)).astype(np.float32))
+    dbuf = to_dev(qkv)
+    strides = [S * 3 * H * D, D, 3 * H * D, 1]
+    desc = g.TensorDesc(BF16, [B, H, S, D], strides)
+    pq = dbuf.p.value
+    pk, pv = pq + 2 * H * D, pq + 4 * H * D
+    ad = g.AttnDesc(causal, D ** -0.5)
+    say(f"attention packed QKV, O over Q, causal={causal}")
+    st = dnn.attention(ad, desc, ctypes.c_void_p(pq), desc, ctypes.c_void_p(pk), desc,
+                       ctypes.c_void_p(pv), desc, ctypes.c_void_p(pq))
+    assert st == g.SUCCESS, g.STATUS[st]
+    g.synchronize()
+    got = dbuf.download(np.uint16, qkv.size).reshape(B, S, 3, H, D)
+    assert np.array_equal(got[:, :, 1:], qkv[:, :, 1:])
+    o = O.bf16_to_f32(got[:, :, 0])
+    x = O.bf16_to_f32(qkv)
+    for b in range(B):
+        for h in range(H):
+            ref = O.attention_head(x[b, :, 0, h], x[b, :, 1, h], x[b, :, 2, h], causal, D ** -0.5)
+            assert normwise_rel_err(o[b, :, h], ref) <= 1e-2, (b, h)
 
 
 def test_attention_key_permutation_invariant(dnn):
