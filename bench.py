@@ -29,7 +29,16 @@ its own launches). The line reports the pre-heat time as "preheat_s".
 
 The CPU baseline (rank 0, N=1) times the oracle -- the reference's own CPU
 GEMM loop restated in C (ref tests/libs/test_grxblas_ex.cpp:45-63) -- on a
-bounded slice of the same workload on the host's cores.
+bounded slice of the same workload on the host's cores. BASELINE config 1
+(fp32 Sgemm 512^3) is the line "sgemm_fp32_512_config1": the GPU library's
+grxblasSgemm, with its stated execution mode -- the CPU host backend
+(oracle/libgrxblas_ref.so) -- timed beside it as that line's CPU baseline.
+
+The matrix-core lines carry the shader clock their kernel ran at ("clock":
+s_memtime spans from the kernels' cycle probe over one launch's event time)
+and the fraction of peak at that clock ("roofline.frac_at_clock"). After the product's GPU timing, the same GEMM
+problems run through torch (hipBLASLt) in a child process and are reported
+beside the product lines ("vendor"); --no-vendor skips that.
 """
 from __future__ import annotations
 
@@ -60,6 +69,59 @@ def log(msg: str) -> None:
 WARM_SECONDS = 0.25   # auto warm-up: at least this much back-to-back work
 PREHEAT_SECONDS = 0.5  # all workloads in turn before the first measurement
 LAST_WARMUP = [0]     # warm-up launches of the latest measurement
+LAST_CLOCK = [None]   # shader clock of the latest measurement (probed_clock)
+NOMINAL_MHZ = 2400.0  # the clock MI355X's peak figures are quoted at
+
+
+def probed_clock(set_probe, slots_needed: int, stream: g.Stream, launch) -> dict | None:
+    """The shader clock one launch ran at, from the kernels' own cycle probe
+    (grxCycleSlot: s_memtime at each wave's start and end, and the CU it ran
+    on). The s_memtime counters of different CUs, even in one XCD, are not
+    synchronized (measured: starts 1e8 ticks apart within one launch), so
+    spans are taken per CU only: from the first wave's start to the last
+    wave's end on that CU, over the launch's HIP-event time. A CU is busy for
+    at most the launch's time, and the event time also holds the launch's
+    fixed overhead, so each figure errs low, never above the true clock; the
+    line reports the median over CUs. Run right after the timed launches,
+    with the GPU at their operating point."""
+    n = int(slots_needed)
+    if n <= 0:
+        return None
+    buf = g.DeviceBuffer(n * ctypes.sizeof(g.CycleSlot))
+    buf.memset(0)
+    try:
+        if set_probe(buf.p, n) != 0:
+            return None
+        launch()                       # a first probed launch: warm the probe's lines
+        g.synchronize()
+        buf.memset(0)
+        e0, e1 = g.Event(), g.Event()
+        e0.record(stream.s)
+        launch()
+        e1.record(stream.s)
+        ms = e0.elapsed_ms(e1)
+        g.synchronize()
+        e0.close()
+        e1.close()
+    finally:
+        set_probe(None, 0)
+    raw = buf.download(np.uint8, n * ctypes.sizeof(g.CycleSlot))
+    buf.close()
+    dt = np.dtype([("start", "<u8"), ("end", "<u8"), ("core", "<u4"), ("warp", "<u4")])
+    sl = raw.view(dt)
+    sl = sl[(sl["start"] != 0) | (sl["end"] != 0)]
+    if sl.size == 0 or ms <= 0:
+        return None
+    spans = []
+    for c in np.unique(sl["core"]):
+        m = sl[sl["core"] == c]
+        spans.append(int(m["end"].max()) - int(m["start"].min()))
+    mhz = [sp / (ms * 1e3) for sp in spans]
+    return {"mhz": round(float(np.median(mhz)), 1), "min_mhz": round(min(mhz), 1),
+            "max_mhz": round(max(mhz), 1), "cus": len(spans),
+            "xcds": int(np.unique(sl["core"] >> 16).size), "launch_ms": round(ms, 4),
+            "source": "s_memtime span per CU (cycle probe, one launch after the timed ones) / "
+                      "that launch's HIP-event time; median over CUs (a lower bound per CU)"}
 
 
 def time_launches(stream: g.Stream, launch, steps: int, warmup: int | None) -> float:
@@ -137,9 +199,15 @@ def roofline(bound: str, work: float, ms: float, peak_key: str, traffic_key: str
         unit = "TOP/s" if peak_key == "int8" else "TFLOP/s"
     peak = PEAK[peak_key]
     traffic = traffic_from_profiles(traffic_key)
-    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": traffic,
-            "traffic_source": TRAFFIC_SOURCE if traffic is not None else None}
+    r = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+         "frac": round(achieved / peak, 4), "traffic": traffic,
+         "traffic_source": TRAFFIC_SOURCE if traffic is not None else None}
+    clock = LAST_CLOCK[0]
+    if bound == "mfma" and clock:
+        # the matrix cores' peak scales with the shader clock: the fraction of
+        # the peak at the clock the kernel actually ran at
+        r["frac_at_clock"] = round(achieved / (peak * clock["mhz"] / NOMINAL_MHZ), 4)
+    return r
 
 
 # ---- CPU baseline -------------------------------------------------------------
@@ -254,22 +322,30 @@ def cpu_attention_baseline(q, k, v, S, D, rows=256):
 
 class Workload:
     def __init__(self, name, unit, bound, peak_key, traffic_key, work, launch, buffers,
-                 cpu=None, ms_digits=4):
+                 cpu=None, ms_digits=4, clock=None):
         self.name, self.unit, self.bound = name, unit, bound
         self.peak_key, self.traffic_key, self.work = peak_key, traffic_key, work
         self.launch, self.buffers, self.cpu, self.ms_digits = launch, buffers, cpu, ms_digits
+        self.clock = clock   # (set_probe, slots) for probed_clock, or None
 
     def measure(self, stream, steps, warmup) -> dict:
         log(f"{self.name}: timing")
         ms = time_launches(stream, self.launch, steps, warmup)
+        LAST_CLOCK[0] = probed_clock(*self.clock, stream, self.launch) if self.clock else None
         scale = 1e6 if self.unit == "GB/s" else 1e9
         return {"name": self.name, "ms": round(ms, self.ms_digits), "warmup": LAST_WARMUP[0],
                 "value": round(self.work / ms / scale, 2 if scale == 1e9 else 1), "unit": self.unit,
-                "roofline": roofline(self.bound, self.work, ms, self.peak_key, self.traffic_key)}
+                "roofline": roofline(self.bound, self.work, ms, self.peak_key, self.traffic_key),
+                "clock": LAST_CLOCK[0]}
 
     def close(self):
         for d in self.buffers:
             d.close()
+
+    def release_device(self):
+        """Free the device buffers once timed (the CPU baseline keeps host copies)."""
+        self.close()
+        self.buffers = []
 
 
 def _checked(status, what):
@@ -289,7 +365,8 @@ def prepare_gemm_bf16(blas, M, cpu_seconds):
         _checked(blas.L.grxblasGemmEx(blas.h, 1, 0, M, N, K, one, dA.p, BF16, K, dB.p, BF16, K, zero,
                                       dC.p, BF16, M), "GemmEx")
     return Workload(f"gemm_bf16_{M}", "TFLOP/s", "mfma", "bf16", f"gemm_bf16_{M}", 2.0 * M * N * K,
-                    launch, [dA, dB, dC], lambda: cpu_gemm_baseline(A, B, M, N, K, cpu_seconds))
+                    launch, [dA, dB, dC], lambda: cpu_gemm_baseline(A, B, M, N, K, cpu_seconds),
+                    clock=(blas.set_cycle_probe, blas.cycle_slots_needed(M, N)))
 
 
 def prepare_sgemm(blas):
@@ -309,6 +386,79 @@ def prepare_sgemm(blas):
                     launch, [dA, dB, dC])
 
 
+_HOST_SGEMM = r"""
+import ctypes, json, os, sys, time
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+import oracle as O
+from grxcp_amd import synth
+ctypes.CDLL(O.HOST_RT, mode=ctypes.RTLD_GLOBAL)
+L = ctypes.CDLL(O.HOST_BLAS)
+fp, vp, i = ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_int
+L.grxblasCreate.argtypes = [ctypes.POINTER(vp)]
+L.grxblasSgemm.argtypes = [vp, i, i, i, i, i, fp, vp, i, vp, i, fp, vp, i]
+h = vp()
+assert L.grxblasCreate(ctypes.byref(h)) == 0
+M = N = K = 512
+A = synth.uniform_f32(M * K, 1, -1.0, 1.0)
+B = synth.uniform_f32(K * N, 2, -1.0, 1.0)
+C = np.zeros(M * N, np.float32)
+one, zero = ctypes.c_float(1.0), ctypes.c_float(0.0)
+p = lambda a: a.ctypes.data_as(vp)
+def call():
+    # row-major C = A B as column-major C^T = B^T A^T (BASELINE config 1)
+    assert L.grxblasSgemm(h, 0, 0, N, M, K, ctypes.byref(one), p(B), N, p(A), K,
+                          ctypes.byref(zero), p(C), N) == 0
+call()
+n, t0 = 0, time.perf_counter()
+while time.perf_counter() - t0 < float(sys.argv[2]):
+    call()
+    n += 1
+dt = time.perf_counter() - t0
+want = A.reshape(M, K).astype(np.float64) @ B.reshape(K, N).astype(np.float64)
+err = float(np.max(np.abs(C.reshape(M, N) - want)) / np.max(np.abs(want)))
+print(json.dumps({"calls": n, "seconds": dt, "rel_err_vs_fp64": err}))
+"""
+
+
+def cpu_host_sgemm_baseline(seconds=5.0):
+    """BASELINE config 1 in its stated execution mode: grxblasSgemm 512^3 on
+    the CPU host backend (oracle/libgrxblas_ref.so, the reference's CPU GEMM
+    loop, ref tests/libs/test_grxblas.cpp:63-80, behind the grxblas.h ABI).
+    Run in a child process: the host backend exports the same symbols as the
+    GPU libraries this process has loaded."""
+    import subprocess
+    threads = cpu_threads()
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads))
+    r = subprocess.run([sys.executable, "-c", _HOST_SGEMM, ROOT, str(seconds)], capture_output=True,
+                       text=True, env=env, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError("host backend Sgemm failed: " + r.stderr[-1000:])
+    v = json.loads(r.stdout.strip().splitlines()[-1])
+    flops = 2.0 * 512 ** 3 * v["calls"]
+    return with_host({"value": round(flops / v["seconds"] / 1e12, 6), "unit": "TFLOP/s",
+                      "cores": threads, "kind": "port",
+                      "sample": f"{v['calls']} calls of grxblasSgemm 512^3 (N,N) on the CPU host "
+                                f"backend (oracle/libgrxblas_ref.so, OpenMP {threads} threads) in "
+                                f"{v['seconds']:.1f} s; max rel err vs fp64 {v['rel_err_vs_fp64']:.2e}"})
+
+
+def prepare_sgemm512(blas):
+    """BASELINE config 1 on the GPU library: fp32 C = A*B, 512^3 row-major,
+    alpha=1 beta=0, U[-1,1] from seeds 1 and 2, as column-major
+    C^T = B^T A^T: Sgemm(N, N, m=512, n=512, k=512, B, 512, A, 512, C, 512)."""
+    M = N = K = 512
+    A = synth.uniform_f32(M * K, 1, -1.0, 1.0)
+    B = synth.uniform_f32(K * N, 2, -1.0, 1.0)
+    dA, dB, dC = g.DeviceBuffer.from_array(A), g.DeviceBuffer.from_array(B), g.DeviceBuffer(M * N * 4)
+    one, zero = g.fptr(1.0), g.fptr(0.0)
+
+    def launch():
+        _checked(blas.L.grxblasSgemm(blas.h, 0, 0, N, M, K, one, dB.p, N, dA.p, K, zero, dC.p, N), "Sgemm")
+    return Workload("sgemm_fp32_512_config1", "TFLOP/s", "mfma", "fp32", "sgemm_fp32_512",
+                    2.0 * M * N * K, launch, [dA, dB, dC], cpu_host_sgemm_baseline, ms_digits=5)
+
+
 def prepare_gemm_int8(blas):
     M, K, N = 4096, 8192, 28672
     log("int8 GEMM + dequant: generating inputs")
@@ -322,7 +472,8 @@ def prepare_gemm_int8(blas):
         _checked(blas.L.grxblasGemmExDequant(blas.h, 1, 0, M, N, K, dA.p, I8, K, dB.p, I8, K, dS.p,
                                              dY.p, BF16, M), "GemmExDequant")
     w = Workload("gemm_int8_dequant_4096x28672x8192", "TOP/s", "mfma", "int8", "gemm_int8_dequant",
-                 2.0 * M * N * K, launch, [dA, dB, dS, dY], lambda: cpu_igemm_baseline(A, B, M, N, K))
+                 2.0 * M * N * K, launch, [dA, dB, dS, dY], lambda: cpu_igemm_baseline(A, B, M, N, K),
+                 clock=(blas.set_cycle_probe, blas.cycle_slots_needed(M, N)))
     return w
 
 
@@ -393,13 +544,108 @@ def prepare_attention(dnn):
         q, k, v = (O.bf16_to_f32(a).reshape(S, D) for a in (q0, k0, v0))
         return cpu_attention_baseline(q, k, v, S, D)
     return Workload("attention_causal_b4h32s4096d128", "TFLOP/s", "mfma", "bf16", "attention",
-                    4.0 * D * B * H * S * (S + 1) / 2, launch, [dq, dk, dv, do], cpu)
+                    4.0 * D * B * H * S * (S + 1) / 2, launch, [dq, dk, dv, do], cpu,
+                    clock=(dnn.set_cycle_probe, dnn.attention_cycle_slots_needed(B, H, S)))
 
 
 SGEMM_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096, 4096, 4096),
                 (4608, 4608, 4608), (5120, 5120, 5120), (6144, 6144, 6144), (8192, 8192, 4096),
                 (1024, 1024, 8192), (2048, 2048, 8192), (4096, 4096, 1024), (6144, 6144, 2048),
                 (4000, 4100, 1000)]
+
+
+def vendor_lines(steps: int) -> int:
+    """The same problems through the vendor libraries, for comparison in the
+    same bench run (run by main() as a child process after its own GPU timing,
+    so that torch's HIP runtime never hosts the product's measurements):
+    torch.mm in bf16 at 8192^3 and 4096^3 with both operands K-contiguous
+    (the product's TN layout; torch dispatches to hipBLASLt), torch._int_mm
+    at config 3's int32 stage (4096 x 28672 x 8192, A row-major, B
+    K-contiguous), and config 3's per-channel dequant as the unfused torch
+    elementwise ops it would take (int32 * fp32 scale -> bf16), timed
+    separately. Each after WARM_SECONDS of warm-up, torch events around
+    `steps` calls. One JSON line per problem. (No clock figure: the vendor
+    kernels carry no cycle probe.)"""
+    import torch
+    gen = torch.Generator(device="cuda").manual_seed(7)
+
+    def timed(fn):
+        t_end = time.perf_counter() + WARM_SECONDS
+        while time.perf_counter() < t_end:
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps, None
+
+    def emit(name, what, ms, work, unit, peak_key, clock):
+        rate = work / ms / 1e9
+        print(json.dumps({"vendor": name, "what": what, "ms": round(ms, 4), "value": round(rate, 2),
+                          "unit": unit, "frac": round(rate / PEAK[peak_key], 4)}), flush=True)
+
+    for M in (8192, 4096):
+        a = torch.randn(M, M, device="cuda", generator=gen).to(torch.bfloat16)
+        bt = torch.randn(M, M, device="cuda", generator=gen).to(torch.bfloat16)
+        c = torch.empty(M, M, device="cuda", dtype=torch.bfloat16)
+        ms, clk = timed(lambda: torch.mm(a, bt.t(), out=c))
+        emit(f"gemm_bf16_{M}", f"torch.mm bf16 {M}^3, A row-major x B K-contiguous (hipBLASLt), bf16 out",
+             ms, 2.0 * M ** 3, "TFLOP/s", "bf16", clk)
+        del a, bt, c
+    M, K, N = 4096, 8192, 28672
+    a = torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8, generator=gen)
+    bt = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=gen)
+    scale = torch.rand(N, device="cuda", generator=gen) * 0.009 + 0.001
+    try:
+        acc = torch._int_mm(a, bt.t())
+        ms, clk = timed(lambda: torch._int_mm(a, bt.t()))
+        emit("gemm_int8_int32", "torch._int_mm 4096x28672x8192, int32 out", ms, 2.0 * M * N * K,
+             "TOP/s", "int8", clk)
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        ms, clk = timed(lambda: y.copy_(acc * scale))
+        # the unfused dequant moves the int32 product in, an fp32 temporary out
+        # and back in, and the bf16 result out
+        moved = M * N * (4 + 4 + 4 + 2)
+        print(json.dumps({"vendor": "dequant_int32_to_bf16", "what": "torch (acc * scale) -> bf16, "
+                          "unfused elementwise", "ms": round(ms, 4),
+                          "GB/s": round(moved / ms / 1e6, 1)}), flush=True)
+    except RuntimeError as e:
+        print(json.dumps({"vendor": "gemm_int8_int32", "error": str(e)[:300]}), flush=True)
+    return 0
+
+
+def run_vendor(steps: int) -> dict:
+    """vendor_lines in a child process; {name: line}. Empty if torch is
+    absent or the child fails."""
+    import subprocess
+    try:
+        import importlib.util
+        if importlib.util.find_spec("torch") is None:
+            return {}
+    except Exception:  # noqa: BLE001
+        return {}
+    log("vendor comparison (torch / hipBLASLt) in a child process")
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-only", "--steps",
+                            str(steps)], capture_output=True, text=True, timeout=900)
+    except subprocess.TimeoutExpired:
+        log("vendor comparison timed out")
+        return {}
+    if r.returncode != 0:
+        log("vendor comparison failed: " + r.stderr[-500:])
+        return {}
+    out = {}
+    for line in r.stdout.splitlines():
+        try:
+            d = json.loads(line)
+        except ValueError:
+            continue
+        if "vendor" in d:
+            out[d["vendor"]] = d
+    return out
 
 
 def sgemm_shapes(steps: int) -> int:
@@ -513,12 +759,18 @@ def main() -> int:
                     help="print the streaming rates of plain device kernels (torch copy, read-only "
                          "sum, fill) on the norms' 16384x8192 bf16 footprint: the ceiling the "
                          "HBM-bound lines are compared against")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip the vendor comparison (torch / hipBLASLt in a child process)")
+    ap.add_argument("--vendor-only", action="store_true",
+                    help="only print the vendor comparison lines (what the child process runs)")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy kernel of MIB MiB (torch), "
                          "the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.stream_ceiling:
         return stream_ceiling(args.steps)
+    if args.vendor_only:
+        return vendor_lines(args.steps)
     if args.calibration_copy:
         import torch
         n = args.calibration_copy * (1 << 20)
@@ -558,12 +810,13 @@ def main() -> int:
         "layernorm": lambda: prepare_norm(dnn, True),
         "attention": lambda: prepare_attention(dnn),
         "sgemm": lambda: prepare_sgemm(blas),
+        "sgemm512": lambda: prepare_sgemm512(blas),
         "softmax": lambda: prepare_rowop(dnn, "softmax"),
         "gelu": lambda: prepare_rowop(dnn, "gelu"),
     }
-    report_order = ["gemm", "gemm4096", "int8", "rmsnorm", "layernorm", "attention", "sgemm",
-                    "softmax", "gelu"]
-    run_order = ["sgemm", "softmax", "gelu", "gemm4096", "int8", "rmsnorm", "layernorm",
+    report_order = ["gemm", "gemm4096", "int8", "rmsnorm", "layernorm", "attention", "sgemm512",
+                    "sgemm", "softmax", "gelu"]
+    run_order = ["sgemm512", "sgemm", "softmax", "gelu", "gemm4096", "int8", "rmsnorm", "layernorm",
                  "attention", "gemm"]
     selected = [k for k in report_order if want(k)]
     loads = {k: makers[k]() for k in selected}          # inputs resident in HBM
@@ -575,6 +828,15 @@ def main() -> int:
     for k in run_order:
         if k in loads:
             results[k] = loads[k].measure(stream, args.steps, args.warmup)
+    for w in loads.values():
+        w.release_device()
+    if not args.no_vendor and any(k in results for k in ("gemm", "gemm4096", "int8")):
+        vendor = run_vendor(args.steps)
+        for k, names in (("gemm", ["gemm_bf16_8192"]), ("gemm4096", ["gemm_bf16_4096"]),
+                         ("int8", ["gemm_int8_int32", "dequant_int32_to_bf16"])):
+            got = [vendor[n] for n in names if n in vendor]
+            if k in results and got:
+                results[k]["vendor"] = got
     if cpu:
         for k in run_order:
             w = loads.get(k)
@@ -616,6 +878,8 @@ def main() -> int:
         "data": "synthetic: seeded N(0,1) bf16 (PCG64), resident in HBM before timing",
         "config": config,
         "roofline": headline["roofline"],
+        "clock": headline.get("clock"),
+        "vendor": headline.get("vendor"),
         "cpu_baseline": headline.get("cpu_baseline"),
         "ops": ops,
     }
