@@ -73,17 +73,20 @@ LAST_CLOCK = [None]   # shader clock of the latest measurement (probed_clock)
 NOMINAL_MHZ = 2400.0  # the clock MI355X's peak figures are quoted at
 
 
-def probed_clock(set_probe, slots_needed: int, stream: g.Stream, launch) -> dict | None:
+def probed_clock(set_probe, slots_needed: int, stream: g.Stream, launch, timed_ms: float) -> dict | None:
     """The shader clock one launch ran at, from the kernels' own cycle probe
     (grxCycleSlot: s_memtime at each wave's start and end, and the CU it ran
     on). The s_memtime counters of different CUs, even in one XCD, are not
     synchronized (measured: starts 1e8 ticks apart within one launch), so
     spans are taken per CU only: from the first wave's start to the last
-    wave's end on that CU, over the launch's HIP-event time. A CU is busy for
-    at most the launch's time, and the event time also holds the launch's
-    fixed overhead, so each figure errs low, never above the true clock; the
-    line reports the median over CUs. Run right after the timed launches,
-    with the GPU at their operating point."""
+    wave's end on that CU, over the workload's timed milliseconds per launch
+    (timed_ms: back to back, so launch overhead is hidden and the figure
+    stands for the kernel's duration). A CU is busy for at most the kernel's
+    duration, so each figure errs low; the line reports the median over CUs.
+    The probed launch's own HIP-event time is reported beside it
+    ("launch_ms": it also holds that launch's fixed overhead, which matters
+    for kernels of ~0.1 ms). Run right after the timed launches, with the GPU
+    at their operating point."""
     n = int(slots_needed)
     if n <= 0:
         return None
@@ -116,12 +119,12 @@ def probed_clock(set_probe, slots_needed: int, stream: g.Stream, launch) -> dict
     for c in np.unique(sl["core"]):
         m = sl[sl["core"] == c]
         spans.append(int(m["end"].max()) - int(m["start"].min()))
-    mhz = [sp / (ms * 1e3) for sp in spans]
+    mhz = [sp / (timed_ms * 1e3) for sp in spans]
     return {"mhz": round(float(np.median(mhz)), 1), "min_mhz": round(min(mhz), 1),
             "max_mhz": round(max(mhz), 1), "cus": len(spans),
             "xcds": int(np.unique(sl["core"] >> 16).size), "launch_ms": round(ms, 4),
             "source": "s_memtime span per CU (cycle probe, one launch after the timed ones) / "
-                      "that launch's HIP-event time; median over CUs (a lower bound per CU)"}
+                      "the timed ms per launch; median over CUs (a lower bound per CU)"}
 
 
 def time_launches(stream: g.Stream, launch, steps: int, warmup: int | None) -> float:
@@ -331,7 +334,7 @@ class Workload:
     def measure(self, stream, steps, warmup) -> dict:
         log(f"{self.name}: timing")
         ms = time_launches(stream, self.launch, steps, warmup)
-        LAST_CLOCK[0] = probed_clock(*self.clock, stream, self.launch) if self.clock else None
+        LAST_CLOCK[0] = probed_clock(*self.clock, stream, self.launch, ms) if self.clock else None
         scale = 1e6 if self.unit == "GB/s" else 1e9
         return {"name": self.name, "ms": round(ms, self.ms_digits), "warmup": LAST_WARMUP[0],
                 "value": round(self.work / ms / scale, 2 if scale == 1e9 else 1), "unit": self.unit,
