@@ -49,11 +49,24 @@ def test_reference_gate_passes_on_mi355x(gpu, name):
 
 def test_reference_cycle_benchmark_runs_on_mi355x(gpu):
     """The cycle benchmark reads per-wave s_memtime slots through the
-    reference's grxCycleSlot ABI at every shape. Its exit gate compares
-    GRX-G100 model cycles (GemmEx <= 1/5 of sgemm's cycles per element); the
-    MI355X's tiny-shape cycles say nothing about that model, so only the
-    measurement checks are asserted here."""
+    reference's grxCycleSlot ABI at every shape. Its exit gate (GemmEx at no
+    more than a fifth of sgemm's cycles per element, ref
+    tests/bench/gemm_cycles.cpp:238-299) and its two k-sweep checks state the
+    reference's simulator model; on gfx950 both calls are one workgroup of
+    fixed cost at these shapes, and all three fail (GemmEx 0.4-0.55x of
+    Sgemm per element; profiles/reference_gemm_cycles_gate.md). Asserted:
+    the two measurement checks that hold, and that those three are the only
+    failures."""
     r = _run("gemm_cycles")
-    assert r.returncode in (0, 1), (r.returncode, r.stderr[-2000:])
-    assert "ok    every shape produced a measurement" in r.stdout, r.stdout[-3000:]
-    assert "ok    the tensor path was measured at every shape" in r.stdout
+    assert r.returncode == 1, (r.returncode, r.stdout[-3000:], r.stderr[-2000:])
+    out = r.stdout
+    assert "ok    every shape produced a measurement" in out, out[-3000:]
+    assert "ok    the tensor path was measured at every shape" in out
+    fails = sorted(line.strip()[len("FAIL"):].strip() for line in out.splitlines()
+                   if line.strip().startswith("FAIL  "))
+    assert fails == sorted([
+        "GemmEx costs at most a fifth of sgemm per output element",
+        "cost per element grows with k",
+        "cost per multiply-add is roughly constant, as an unblocked loop should be",
+    ]), fails
+    assert "FAILED (3)" in out
