@@ -6,11 +6,12 @@
 //
 //  * gemm_tn_fast: op(A) and op(B) both K-contiguous (transa=T, transb=N in
 //    grxBLAS's column-major terms, i.e. row-major A times column-major B). A
-//    256x256 macro tile per 256-thread workgroup (4 waves, 128x128 each, 4x4
-//    v_mfma 32x32 tiles per wave), 128 bytes of K per stage (64 bf16/fp16 or
-//    128 int8), two LDS stages of 64 KB, 16-byte buffer loads, an XOR swizzle
-//    that keeps ds_read_b128 / ds_write_b128 free of bank conflicts, and an
-//    XCD-aware tile order. Ragged m/n are handled by the buffer descriptor's
+//    256x256 macro tile per 256-thread workgroup (4 waves, 128x128 each: 8x8
+//    v_mfma 16x16 tiles per wave for bf16/fp16/int8, 4x4 32x32 tiles for
+//    fp32), 128 bytes of K per stage (64 bf16/fp16 or 128 int8), two LDS
+//    stages of 64 KB, 16-byte buffer loads, an XOR swizzle that keeps
+//    ds_read_b128 / ds_write_b128 free of bank conflicts, and an XCD-aware
+//    tile order. Ragged m/n are handled by the buffer descriptor's
 //    range check (out-of-range rows read as zero) plus masked stores; a ragged
 //    k is masked per 16-byte chunk, so k only has to be a multiple of 16 bytes.
 //
@@ -23,12 +24,13 @@
 // Both kernels are byte-generic: every matrix-core step consumes 16 bytes of
 // A and 16 bytes of B per lane (8 bf16/fp16 or 16 int8 in one v_mfma, 4 fp32
 // in four v_mfma_f32_32x32x2_f32) and produces the same 32x32 accumulator
-// layout, so one body serves all four input types. fp32 serves Sgemm's
-// problems that fill the GPU (grxblas.cpp sgemm_batched).
+// layout, so one body serves all four input types; gemm_tn_fast's 16x16
+// path likewise for the 16-bit and int8 types. fp32 serves Sgemm's problems
+// that fill the GPU (grxblas.cpp sgemm_batched).
 //
-// Accumulator layout of a 32x32 MFMA (verified on gfx950 by
-// tests/test_gpu_gemm.py): lane l, element r holds row
-// 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// Accumulator layouts (verified on gfx950 by tests/test_gpu_gemm.py): 32x32
+// MFMA, lane l, element r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32;
+// 16x16 MFMA, row 4*(l/16) + r, column l%16.
 
 #include "../launch.h"
 #include "device_common.h"
@@ -54,6 +56,14 @@ struct OpBF16 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // gemm_tn_fast: 16x16 tiles, accumulated in place in AGPRs (assembly, so
+  // that the register allocator cannot move an accumulator between k-steps:
+  // with the builtin it copied 80 of them per loop trip).
+  static constexpr bool kM16 = true;
+  using Acc16 = f32x4;
+  __device__ static void mma16(i32x4 a, i32x4 b, Acc16& c) {
+    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
 };
 
 struct OpF16 {
@@ -65,6 +75,14 @@ struct OpF16 {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
+  // gemm_tn_fast: 16x16 tiles, accumulated in place in AGPRs (assembly, so
+  // that the register allocator cannot move an accumulator between k-steps:
+  // with the builtin it copied 80 of them per loop trip).
+  static constexpr bool kM16 = true;
+  using Acc16 = f32x4;
+  __device__ static void mma16(i32x4 a, i32x4 b, Acc16& c) {
+    asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
 };
 
 struct OpI8 {
@@ -74,6 +92,14 @@ struct OpI8 {
   static constexpr int kElemBytes = 1;
   __device__ static Acc mma(i32x4 a, i32x4 b, Acc c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+  // gemm_tn_fast: 16x16 tiles, accumulated in place in AGPRs (assembly, so
+  // that the register allocator cannot move an accumulator between k-steps:
+  // with the builtin it copied 80 of them per loop trip).
+  static constexpr bool kM16 = true;
+  using Acc16 = i32x4;
+  __device__ static void mma16(i32x4 a, i32x4 b, Acc16& c) {
+    asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
   }
 };
 
@@ -92,6 +118,9 @@ struct OpF32 {
     for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s], bf[s], c, 0, 0, 0);
     return c;
   }
+  // gemm_tn_fast keeps 32x32 tiles for fp32 (with v_mfma_f32_16x16x4 one
+  // wave per SIMD runs out of registers).
+  static constexpr bool kM16 = false;
 };
 
 struct KParams {
@@ -429,240 +458,380 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
     }
   };
 
-  using Acc = typename Op::Acc;
-  Acc acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
   const int wm = wave >> 1;
   const int wn = wave & 1;
-  const int r32 = lane & 31;
-  const int hh = lane >> 5;
-
-  // Fragment reads: A rows wm*128 + 32t + r32, B rows wn*128 + 32t + r32,
-  // 16 bytes at logical chunk 2*ks + hh. Two register sets: the reads for
-  // k-step ks+1 are in flight while the 16 MFMAs of k-step ks run. Read slot
-  // q follows first use in the next k-step (A0, B0..B3, A1..A3), so each
-  // read has at least five MFMA pairs to land before an MFMA needs it.
-  // The LDS byte address of every stage-0 fragment a lane reads ([tile]
-  // [k-step], A and B) is computed once; a read of stage 1 adds 32 KB in the
-  // instruction's offset field. With the stage a compile-time constant (the
-  // main loop below is unrolled by two), fragment reads cost no VALU
-  // instruction (measured 1-2 % faster than computing each address); the
-  // masked tail reads with a run-time stage.
-  i32x4 fa[2][4], fb[2][4];
   typedef __attribute__((address_space(3))) const i32x4* lds_frag_t;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][0][0];
   constexpr uint32_t kStageBytes = kFastTile * kChunks * 16;    // 32 KB
-  uint32_t ad_a[4][4], ad_b[4][4];                               // stage 0, [tile][k-step]
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int kc = 2 * ks + hh;
-      const int ar = wm * 128 + t * 32 + r32;
-      const int br = wn * 128 + t * 32 + r32;
-      ad_a[t][ks] = lds0 + 16u * (uint32_t)(ar * kChunks + (kc ^ swz(ar)));
-      ad_b[t][ks] = lds0 + 2 * kStageBytes + 16u * (uint32_t)(br * kChunks + (kc ^ swz(br)));
-    }
-  auto frag = [&](auto st, int ks, int buf, int q) {
-    const int t = (q >= 1 && q <= 4) ? q - 1 : (q == 0 ? 0 : q - 4);
-    if constexpr (std::is_integral<decltype(st)>::value) {
-      const int kc = 2 * ks + hh;
-      if (q >= 1 && q <= 4) {
-        const int br = wn * 128 + t * 32 + r32;
-        fb[buf][t] = lds[1][st][br * kChunks + (kc ^ swz(br))];
-      } else {
-        const int ar = wm * 128 + t * 32 + r32;
-        fa[buf][t] = lds[0][st][ar * kChunks + (kc ^ swz(ar))];
-      }
-    } else {
-      constexpr uint32_t off = decltype(st)::value * kStageBytes;
-      if (q >= 1 && q <= 4) fb[buf][t] = *(lds_frag_t)(uintptr_t)(ad_b[t][ks] + off);
-      else fa[buf][t] = *(lds_frag_t)(uintptr_t)(ad_a[t][ks] + off);
-    }
-  };
 
   // A stage is 16 DMA instructions, d = 0..15: 8-row block group
   // 4*(d/8) + d%4 of operand (d/4)%2.
-  auto dma_d = [&](int kt, int st, int d, auto full) {
+  auto dma_d = [&](int kt, int st, int d, auto full) __attribute__((always_inline)) {
     dma(kt, st, 4 * (d >> 3) + (d & 3), (d >> 2) & 1, full);
   };
-
-  // One k-step: 16 MFMAs on register set `buf` in 8 slots of one MFMA pair.
-  // In the phases that carry DMA, DMA instructions d0 .. d0+cnt-1 are spread
-  // evenly over the slots, each issued ahead of its slot's MFMA pair: a DMA
-  // issue that waits for the address unit then waits while the previous
-  // pair still runs (measured 1-3 % faster than issuing it after the pair;
-  // moving the fragment read ahead as well is 3 % slower). Behind every pair
-  // one fragment read for the next k-step. The order is held by
-  // sched_barrier.
-  auto phase = [&](int buf, auto rd_st, int rd_ks, int dma_kt, int dma_st, int d0, int cnt, auto full) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      // int8: snake order (B reversed on odd A rows, so consecutive MFMAs
-      // never change both operands; +0.5 % on config-3 int8, same run, both
-      // library orders). The 16-bit types keep the plain order (snake: bf16
-      // 8192^3 +-0.1 %, 4096^3 -0.5 ... -2.5 %). Each accumulator's k order,
-      // and so every result, is the same either way.
-      constexpr bool kSnake = std::is_same<Op, OpI8>::value;
-      const int i = q >> 1;
-      const bool rev = kSnake && (i & 1) != 0;
-      const int ja = rev ? 3 - 2 * (q & 1) : 2 * (q & 1);
-      const int jb = rev ? ja - 1 : ja + 1;
-      if ((q + 1) * cnt / 8 > q * cnt / 8) dma_d(dma_kt, dma_st, d0 + q * cnt / 8, full);
-      __builtin_amdgcn_sched_barrier(0);
-      acc[i][ja] = Op::mma(fa[buf][i], fb[buf][ja], acc[i][ja]);
-      acc[i][jb] = Op::mma(fa[buf][i], fb[buf][jb], acc[i][jb]);
-      frag(rd_st, rd_ks, buf ^ 1, q);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  // Stage s lives in LDS buffer s & 1. Iteration kt runs k-steps 0..2 of
-  // stage kt, one barrier, then k-step 3. Stage kt+2's DMA (into the buffer
-  // stage kt just vacated) is issued half right after that barrier and half
-  // during k-step 0 of the next iteration, so each load has two to four
-  // k-steps of MFMA time to land before the barrier that publishes it.
-  // (Measured: moving part of it into k-step 1 saves less DMA issue time
-  // than the late loads then cost at the barrier.)
-  constexpr int kDmaD = 8, kDmaA = 8;
-#pragma unroll
-  for (int d = 0; d < 16; ++d) dma_d(0, 0, d, std::false_type{});
-#pragma unroll
-  for (int d = 0; d < kDmaD; ++d) dma_d(1, 1, d, std::false_type{});
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaD) : "memory");  // stage 0 landed
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < 8; ++q) frag(IntC<0>{}, 0, 0, q);
-
-  auto iter_c = [&](int kt, auto stage) __attribute__((always_inline)) {
-    constexpr int cur = decltype(stage)::value;
-    phase(0, IntC<cur>{}, 1, kt + 1, cur ^ 1, kDmaD, kDmaA, std::true_type{});
-    phase(1, IntC<cur>{}, 2, 0, 0, 0, 0, std::true_type{});
-    phase(0, IntC<cur>{}, 3, 0, 0, 0, 0, std::true_type{});
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 landed
-    __syncthreads();
-    phase(1, IntC<cur ^ 1>{}, 0, kt + 2, cur, 0, kDmaD, std::true_type{});
-  };
-  auto iter_r = [&](int kt) __attribute__((always_inline)) {
-    const int cur = kt & 1;
-    phase(0, cur, 1, kt + 1, cur ^ 1, kDmaD, kDmaA, std::false_type{});
-    phase(1, cur, 2, 0, 0, 0, 0, std::false_type{});
-    phase(0, cur, 3, 0, 0, 0, 0, std::false_type{});
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 landed
-    __syncthreads();
-    phase(1, cur ^ 1, 0, kt + 2, cur, 0, kDmaD, std::false_type{});
-  };
-  // While the stages an iteration loads (kt+1, kt+2) lie wholly inside K,
-  // its DMAs need no mask and its stage is known at compile time (two
-  // iterations per trip); the rest take the masked form.
+  // While the stages an iteration loads lie wholly inside K, its DMAs need
+  // no mask and its stage is known at compile time (two iterations per
+  // trip); the rest take the masked form.
   const int kfull = kbytes / kFastKBytes;
-  int kt = 0;
-  for (; kt + 3 < kfull; kt += 2) {
-    iter_c(kt, IntC<0>{});
-    iter_c(kt + 1, IntC<1>{});
-  }
-  for (; kt < ktiles; ++kt) iter_r(kt);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // no LDS write may outlive the loop
-  __syncthreads();                                     // and no wave still reads a stage
 
-  // Epilogue through LDS. A lane's accumulators are 4-row pieces of 32
-  // different columns; stored as they are, every vector store would touch 32
-  // cache lines 16 bytes at a time. Instead each wave parks one 128x32 column
-  // block of raw 32-bit accumulators in its own LDS region ([col][row], pitch
-  // 132 words) and reads it back as runs of kRun rows of one column, so one
-  // store instruction writes whole 256-byte (or 512-byte) column segments.
-  // Rows 64..127 sit 4 words further on (row r at r + 4*(r/64 & 1)): that
-  // keeps the 16 lanes of one column on distinct banks when they read their
-  // runs, with every offset on the write side a compile-time constant.
+  // Epilogue through LDS. A lane's accumulators are 4-row pieces of 16 or 32
+  // different columns; stored as they are, every vector store would touch
+  // that many cache lines 16 bytes at a time. Instead each wave parks one
+  // 128x32 column block of raw 32-bit accumulators in its own LDS region
+  // ([col][row], pitch 132 words; `park` writes it) and reads it back as
+  // runs of kRun rows of one column, so one store instruction writes whole
+  // 256-byte (or 512-byte) column segments. Rows 64..127 sit 4 words further
+  // on (row r at r + 4*(r/64 & 1)): that keeps the 16 lanes of one column on
+  // distinct banks when they read their runs, with every offset on the
+  // write side a compile-time constant.
   using E = typename Op::Elem;
   constexpr int kRun = Epi<OUT>::kRun;            // 8 (16-bit C) or 4 (32-bit C)
   constexpr int kPitch = 128 + 4;
   constexpr int kLanesPerCol = 128 / kRun;        // 16 or 32
   constexpr int kColsPerRound = 64 / kLanesPerCol;
   int* stage = (int*)&lds[0][0][0] + wave * 32 * kPitch;   // 16.5 KB per wave
-  const int run = lane % kLanesPerCol;
-  const int rcol = lane / kLanesPerCol;
-  const int run_pos = run * kRun + 4 * ((run * kRun >> 6) & 1);
-  const int gi = row0 + wm * 128 + run * kRun;
-  // Dequant: the 32 column scales this lane applies (4 column blocks x the
-  // 32 / kColsPerRound runs of each), loaded together as the epilogue starts
-  // so their latency overlaps the first block's LDS round trip, instead of
-  // one dependent load per run (config-3 int8: the epilogue took 15.6K
-  // cycles per tile against bf16's 9.7K for the same output; +0.8 % end to
-  // end, bit-identical).
-  constexpr bool kDeq = OUT == MmaOut::DEQ_BF16;
-  constexpr int kRunsPerBlock = 32 / kColsPerRound;
-  float dscale[kDeq ? 4 : 1][kDeq ? kRunsPerBlock : 1];
-  if constexpr (kDeq) {
+  auto epilogue = [&](auto park) __attribute__((always_inline)) {
+    const int run = lane % kLanesPerCol;
+    const int rcol = lane / kLanesPerCol;
+    const int run_pos = run * kRun + 4 * ((run * kRun >> 6) & 1);
+    const int gi = row0 + wm * 128 + run * kRun;
+    // Dequant: the 32 column scales this lane applies (4 column blocks x the
+    // 32 / kColsPerRound runs of each), loaded together as the epilogue
+    // starts so their latency overlaps the first block's LDS round trip,
+    // instead of one dependent load per run (config-3 int8: the epilogue took
+    // 15.6K cycles per tile against bf16's 9.7K for the same output; +0.8 %
+    // end to end, bit-identical).
+    constexpr bool kDeq = OUT == MmaOut::DEQ_BF16;
+    constexpr int kRunsPerBlock = 32 / kColsPerRound;
+    float dscale[kDeq ? 4 : 1][kDeq ? kRunsPerBlock : 1];
+    if constexpr (kDeq) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int rd = 0; rd < kRunsPerBlock; ++rd) {
-        const int gj = col0 + wn * 128 + 32 * j + rd * kColsPerRound + rcol;
-        dscale[j][rd] = gj < p.n ? p.scale[gj] : 0.0f;
+        for (int rd = 0; rd < kRunsPerBlock; ++rd) {
+          const int gj = col0 + wn * 128 + 32 * j + rd * kColsPerRound + rcol;
+          dscale[j][rd] = gj < p.n ? p.scale[gj] : 0.0f;
+        }
+    }
+    // One column block per call; J is a compile-time constant so that the
+    // accumulators stay in registers (a run-time index would move them to
+    // scratch).
+    auto column_block = [&](auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      park(jc);
+      // LDS operations of one wave complete in order; the compiler only must
+      // not move the reads above the writes (or the next writes above them).
+      asm volatile("" ::: "memory");
+      auto read_run = [&](int col, E* v) __attribute__((always_inline)) {
+        const int* src = &stage[col * kPitch + run_pos];
+#pragma unroll
+        for (int h = 0; h < kRun / 4; ++h) {
+          const i32x4 w = *(const i32x4*)(src + 4 * h);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[4 * h + q] = from_bits<E>(w[q]);
+        }
+      };
+      const int gj0 = col0 + wn * 128 + 32 * j;
+      if (row0 + wm * 128 + 128 <= p.m && gj0 + 32 <= p.n) {
+        // Interior block (the common case): unrolled, no masks.
+        using T = typename Epi<OUT>::T;
+        T* cbase = (T*)p.c + (int64_t)gj0 * p.ldc + gi;
+#pragma unroll
+        for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
+          const int col = rd * kColsPerRound + rcol;
+          E v[kRun];
+          read_run(col, v);
+          if constexpr (kDeq)
+            Epi<OUT>::template put_run_scaled<STREAM>(cbase + (int64_t)col * p.ldc, v, dscale[j][rd]);
+          else
+            Epi<OUT>::template put_run<STREAM>(p, cbase + (int64_t)col * p.ldc, v, gj0 + col);
+        }
+      } else {
+        for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
+          const int col = rd * kColsPerRound + rcol;
+          E v[kRun];
+          read_run(col, v);
+          const int gj = gj0 + col;
+          if (gj < p.n && gi < p.m) store_run<OUT, STREAM>(p, gi, gj, v, kRun, true);
+        }
       }
-  }
-  // One column block per call; J is a compile-time constant so that acc stays
-  // in registers (a run-time index would move the accumulators to scratch).
-  auto column_block = [&](auto jc) __attribute__((always_inline)) {
-    constexpr int j = decltype(jc)::value;
+      asm volatile("" ::: "memory");
+    };
+    column_block(IntC<0>{});
+    column_block(IntC<1>{});
+    column_block(IntC<2>{});
+    column_block(IntC<3>{});
+  };
+
+  if constexpr (Op::kM16) {
+    // 16-bit and int8 inputs: 8 x 8 tiles of 16x16 per wave, 64-byte
+    // k-steps (two per stage). Against 4 x 4 tiles of 32x32 (the fp32 path
+    // below) the same operand bytes move, and the matrix cores draw less
+    // power per FLOP: rocprofv3 over bf16 8192^3 read the same matrix-busy
+    // cycles at a 1.91 GHz clock against 1.65 (+7.5 % sustained).
+    using Acc = typename Op::Acc16;
+    Acc acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = 0;
+    const int r16 = lane & 15;
+    // The k-step's four 16-byte chunks go to the four 16-lane groups in the
+    // order 0, 2, 1, 3 (A and B alike, so every product is unchanged): a
+    // ds_read_b128 serves 32 lanes at a time, and under the row swizzle
+    // chunks c and c+2 of rows 0-15 land on distinct banks where c and c+1
+    // would share them (rocprofv3: 6.8e7 bank-conflict cycles per launch at
+    // 8192^3 in the plain order, none here).
+    const int kq = ((lane >> 3) & 2) | ((lane >> 5) & 1);
+
+    // Fragment reads: A rows wm*128 + 16t + r16, B rows wn*128 + 16t + r16,
+    // 16 bytes at logical chunk 4*ks + kq. A fragments roll: the next
+    // k-step's fragment t is read into the same registers once row t's last
+    // MFMA has issued. B fragments are double-buffered. The LDS byte address
+    // of every stage-0 fragment is computed once; stage 1 adds 32 KB, in the
+    // instruction's offset field where the stage is a compile-time constant.
+    i32x4 fa[8], fb[2][8];
+    uint32_t ad_a[8][2], ad_b[8][2];                               // stage 0, [tile][k-step]
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int kc = 4 * ks + kq;
+        const int ar = wm * 128 + t * 16 + r16;
+        const int br = wn * 128 + t * 16 + r16;
+        ad_a[t][ks] = lds0 + 16u * (uint32_t)(ar * kChunks + (kc ^ swz(ar)));
+        ad_b[t][ks] = lds0 + 2 * kStageBytes + 16u * (uint32_t)(br * kChunks + (kc ^ swz(br)));
+      }
+    auto frag_a = [&](auto st, int ks, int t) __attribute__((always_inline)) {
+      if constexpr (std::is_integral<decltype(st)>::value)
+        fa[t] = *(lds_frag_t)(uintptr_t)(ad_a[t][ks] + (uint32_t)st * kStageBytes);
+      else
+        fa[t] = *(lds_frag_t)(uintptr_t)(ad_a[t][ks] + decltype(st)::value * kStageBytes);
+    };
+    auto frag_b = [&](auto st, int ks, int buf, int t) __attribute__((always_inline)) {
+      if constexpr (std::is_integral<decltype(st)>::value)
+        fb[buf][t] = *(lds_frag_t)(uintptr_t)(ad_b[t][ks] + (uint32_t)st * kStageBytes);
+      else
+        fb[buf][t] = *(lds_frag_t)(uintptr_t)(ad_b[t][ks] + decltype(st)::value * kStageBytes);
+    };
+
+    // One k-step: 64 MFMAs in 32 slots of one MFMA pair (A row i = q/4).
+    // DMA instructions d0 .. d0+cnt-1 are spread evenly, each ahead of its
+    // slot's pair; behind the pair, the next k-step's B fragments (the even
+    // slots of the first half) and A fragment i (behind row i's last pair).
+    // The order is held by sched_barrier.
+    auto phase = [&](int buf, auto rd_st, int rd_ks, int dma_kt, int dma_st, int d0, int cnt,
+                     auto full) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < 32; ++q) {
+        const int i = q >> 2;
+        const int ja = 2 * (q & 3), jb = ja + 1;
+        if ((q + 1) * cnt / 32 > q * cnt / 32) dma_d(dma_kt, dma_st, d0 + q * cnt / 32, full);
+        __builtin_amdgcn_sched_barrier(0);
+        Op::mma16(fa[i], fb[buf][ja], acc[i][ja]);
+        Op::mma16(fa[i], fb[buf][jb], acc[i][jb]);
+        __builtin_amdgcn_sched_barrier(0);
+        if ((q & 1) == 0 && q < 16) frag_b(rd_st, rd_ks, buf ^ 1, q >> 1);
+        if ((q & 3) == 3) frag_a(rd_st, rd_ks, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
+    // Stage s lives in LDS buffer s & 1. Iteration kt runs k-step 0 of stage
+    // kt, one barrier (stage kt+1 landed, stage kt no longer read), then
+    // k-step 1 with stage kt+2's 16 DMAs (into the buffer stage kt just
+    // vacated) spread over it, so each load has one to two k-steps of MFMA
+    // time to land. (Measured against this: half of the DMAs in the k-step
+    // before the barrier, as the fp32 path does with its four k-steps per
+    // stage, left the last loads no cover: 67 % matrix-busy against 80 %;
+    // all 16 in the first half of the k-step: -5 %.)
+#pragma unroll
+    for (int d = 0; d < 16; ++d) dma_d(0, 0, d, std::false_type{});
+#pragma unroll
+    for (int d = 0; d < 16; ++d) dma_d(1, 1, d, std::false_type{});
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // stage 0 landed
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      frag_a(IntC<0>{}, 0, t);
+      frag_b(IntC<0>{}, 0, 0, t);
+    }
+    auto iter_c = [&](int kt, auto stage_c) __attribute__((always_inline)) {
+      constexpr int cur = decltype(stage_c)::value;
+      phase(0, IntC<cur>{}, 1, 0, 0, 0, 0, std::true_type{});
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 landed
+      __syncthreads();
+      phase(1, IntC<cur ^ 1>{}, 0, kt + 2, cur, 0, 16, std::true_type{});
+    };
+    auto iter_r = [&](int kt) __attribute__((always_inline)) {
+      const int cur = kt & 1;
+      phase(0, cur, 1, 0, 0, 0, 0, std::false_type{});
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 landed
+      __syncthreads();
+      phase(1, cur ^ 1, 0, kt + 2, cur, 0, 16, std::false_type{});
+    };
+    int kt = 0;
+    for (; kt + 3 < kfull; kt += 2) {
+      iter_c(kt, IntC<0>{});
+      iter_c(kt + 1, IntC<1>{});
+    }
+    for (; kt < ktiles; ++kt) iter_r(kt);
+    // The MFMAs are assembly, so the compiler places the epilogue's reads of
+    // their results without knowing what wrote them: 18 wait states first.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // no LDS write may outlive the loop
+    __syncthreads();                                     // and no wave still reads a stage
+
+    // Lane l holds rows 16i + 4*(l/16) .. +3 of column 16*jj + l%16.
+    epilogue([&](auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          i32x4 w;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) w[q] = bits_of(acc[i][2 * j + h][q]);
+          *(i32x4*)&stage[(16 * h + r16) * kPitch + 16 * i + 4 * (lane >> 4) + 4 * (i >> 2)] = w;
+        }
+    });
+  } else {
+    // fp32: 4 x 4 tiles of 32x32 per wave, 32-byte k-steps (four per stage).
+    using Acc = typename Op::Acc;
+    Acc acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        i32x4 w;
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) w[q] = bits_of(acc[i][j][4 * g + q]);
-        *(i32x4*)&stage[r32 * kPitch + 32 * i + 8 * g + 4 * hh + 4 * (i >> 1)] = w;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    const int r32 = lane & 31;
+    const int hh = lane >> 5;
+
+    // Fragment reads: A rows wm*128 + 32t + r32, B rows wn*128 + 32t + r32,
+    // 16 bytes at logical chunk 2*ks + hh. Two register sets: the reads for
+    // k-step ks+1 are in flight while the 16 MFMAs of k-step ks run. Read
+    // slot q follows first use in the next k-step (A0, B0..B3, A1..A3), so
+    // each read has at least five MFMA pairs to land before an MFMA needs it.
+    // The LDS byte address of every stage-0 fragment a lane reads ([tile]
+    // [k-step], A and B) is computed once; a read of stage 1 adds 32 KB in
+    // the instruction's offset field. With the stage a compile-time constant
+    // (the main loop below is unrolled by two), fragment reads cost no VALU
+    // instruction (measured 1-2 % faster than computing each address); the
+    // masked tail reads with a run-time stage.
+    i32x4 fa[2][4], fb[2][4];
+    uint32_t ad_a[4][4], ad_b[4][4];                               // stage 0, [tile][k-step]
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int kc = 2 * ks + hh;
+        const int ar = wm * 128 + t * 32 + r32;
+        const int br = wn * 128 + t * 32 + r32;
+        ad_a[t][ks] = lds0 + 16u * (uint32_t)(ar * kChunks + (kc ^ swz(ar)));
+        ad_b[t][ks] = lds0 + 2 * kStageBytes + 16u * (uint32_t)(br * kChunks + (kc ^ swz(br)));
       }
-    // LDS operations of one wave complete in order; the compiler only must
-    // not move the reads above the writes (or the next writes above them).
-    asm volatile("" ::: "memory");
-    auto read_run = [&](int col, E* v) __attribute__((always_inline)) {
-      const int* src = &stage[col * kPitch + run_pos];
-#pragma unroll
-      for (int h = 0; h < kRun / 4; ++h) {
-        const i32x4 w = *(const i32x4*)(src + 4 * h);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[4 * h + q] = from_bits<E>(w[q]);
+    auto frag = [&](auto st, int ks, int buf, int q) __attribute__((always_inline)) {
+      const int t = (q >= 1 && q <= 4) ? q - 1 : (q == 0 ? 0 : q - 4);
+      if constexpr (std::is_integral<decltype(st)>::value) {
+        const int kc = 2 * ks + hh;
+        if (q >= 1 && q <= 4) {
+          const int br = wn * 128 + t * 32 + r32;
+          fb[buf][t] = lds[1][st][br * kChunks + (kc ^ swz(br))];
+        } else {
+          const int ar = wm * 128 + t * 32 + r32;
+          fa[buf][t] = lds[0][st][ar * kChunks + (kc ^ swz(ar))];
+        }
+      } else {
+        constexpr uint32_t off = decltype(st)::value * kStageBytes;
+        if (q >= 1 && q <= 4) fb[buf][t] = *(lds_frag_t)(uintptr_t)(ad_b[t][ks] + off);
+        else fa[buf][t] = *(lds_frag_t)(uintptr_t)(ad_a[t][ks] + off);
       }
     };
-    const int gj0 = col0 + wn * 128 + 32 * j;
-    if (row0 + wm * 128 + 128 <= p.m && gj0 + 32 <= p.n) {
-      // Interior block (the common case): unrolled, no masks.
-      using T = typename Epi<OUT>::T;
-      T* cbase = (T*)p.c + (int64_t)gj0 * p.ldc + gi;
+
+    // One k-step: 16 MFMAs on register set `buf` in 8 slots of one MFMA
+    // pair. In the phases that carry DMA, DMA instructions d0 .. d0+cnt-1
+    // are spread evenly over the slots, each issued ahead of its slot's MFMA
+    // pair: a DMA issue that waits for the address unit then waits while the
+    // previous pair still runs (measured 1-3 % faster than issuing it after
+    // the pair; moving the fragment read ahead as well is 3 % slower).
+    // Behind every pair one fragment read for the next k-step. The order is
+    // held by sched_barrier.
+    auto phase = [&](int buf, auto rd_st, int rd_ks, int dma_kt, int dma_st, int d0, int cnt,
+                     auto full) __attribute__((always_inline)) {
 #pragma unroll
-      for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
-        const int col = rd * kColsPerRound + rcol;
-        E v[kRun];
-        read_run(col, v);
-        if constexpr (kDeq)
-          Epi<OUT>::template put_run_scaled<STREAM>(cbase + (int64_t)col * p.ldc, v, dscale[j][rd]);
-        else
-          Epi<OUT>::template put_run<STREAM>(p, cbase + (int64_t)col * p.ldc, v, gj0 + col);
+      for (int q = 0; q < 8; ++q) {
+        const int i = q >> 1;
+        const int ja = 2 * (q & 1), jb = ja + 1;
+        if ((q + 1) * cnt / 8 > q * cnt / 8) dma_d(dma_kt, dma_st, d0 + q * cnt / 8, full);
+        __builtin_amdgcn_sched_barrier(0);
+        acc[i][ja] = Op::mma(fa[buf][i], fb[buf][ja], acc[i][ja]);
+        acc[i][jb] = Op::mma(fa[buf][i], fb[buf][jb], acc[i][jb]);
+        frag(rd_st, rd_ks, buf ^ 1, q);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    } else {
-      for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
-        const int col = rd * kColsPerRound + rcol;
-        E v[kRun];
-        read_run(col, v);
-        const int gj = gj0 + col;
-        if (gj < p.n && gi < p.m) store_run<OUT, STREAM>(p, gi, gj, v, kRun, true);
-      }
+    };
+
+    // Stage s lives in LDS buffer s & 1. Iteration kt runs k-steps 0..2 of
+    // stage kt, one barrier, then k-step 3. Stage kt+2's DMA (into the
+    // buffer stage kt just vacated) is issued half right after that barrier
+    // and half during k-step 0 of the next iteration, so each load has two to
+    // four k-steps of MFMA time to land before the barrier that publishes it.
+    // (Measured: moving part of it into k-step 1 saves less DMA issue time
+    // than the late loads then cost at the barrier.)
+    constexpr int kDmaD = 8, kDmaA = 8;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) dma_d(0, 0, d, std::false_type{});
+#pragma unroll
+    for (int d = 0; d < kDmaD; ++d) dma_d(1, 1, d, std::false_type{});
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaD) : "memory");  // stage 0 landed
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) frag(IntC<0>{}, 0, 0, q);
+
+    auto iter_c = [&](int kt, auto stage_c) __attribute__((always_inline)) {
+      constexpr int cur = decltype(stage_c)::value;
+      phase(0, IntC<cur>{}, 1, kt + 1, cur ^ 1, kDmaD, kDmaA, std::true_type{});
+      phase(1, IntC<cur>{}, 2, 0, 0, 0, 0, std::true_type{});
+      phase(0, IntC<cur>{}, 3, 0, 0, 0, 0, std::true_type{});
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 landed
+      __syncthreads();
+      phase(1, IntC<cur ^ 1>{}, 0, kt + 2, cur, 0, kDmaD, std::true_type{});
+    };
+    auto iter_r = [&](int kt) __attribute__((always_inline)) {
+      const int cur = kt & 1;
+      phase(0, cur, 1, kt + 1, cur ^ 1, kDmaD, kDmaA, std::false_type{});
+      phase(1, cur, 2, 0, 0, 0, 0, std::false_type{});
+      phase(0, cur, 3, 0, 0, 0, 0, std::false_type{});
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt+1 landed
+      __syncthreads();
+      phase(1, cur ^ 1, 0, kt + 2, cur, 0, kDmaD, std::false_type{});
+    };
+    int kt = 0;
+    for (; kt + 3 < kfull; kt += 2) {
+      iter_c(kt, IntC<0>{});
+      iter_c(kt + 1, IntC<1>{});
     }
-    asm volatile("" ::: "memory");
-  };
-  column_block(IntC<0>{});
-  column_block(IntC<1>{});
-  column_block(IntC<2>{});
-  column_block(IntC<3>{});
+    for (; kt < ktiles; ++kt) iter_r(kt);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // no LDS write may outlive the loop
+    __syncthreads();                                     // and no wave still reads a stage
+
+    // Lane l holds rows 32i + 8g + 4*(l/32) .. +3 of column 32j + l%32.
+    epilogue([&](auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          i32x4 w;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) w[q] = bits_of(acc[i][j][4 * g + q]);
+          *(i32x4*)&stage[r32 * kPitch + 32 * i + 8 * g + 4 * hh + 4 * (i >> 1)] = w;
+        }
+    });
+  }
 
   cycle_record(p.probe, t0, probe_slot(wave), wave);
 }
