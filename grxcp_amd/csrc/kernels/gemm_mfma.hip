@@ -627,7 +627,14 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
 #pragma unroll
       for (int q = 0; q < 32; ++q) {
         const int i = q >> 2;
-        const int ja = 2 * (q & 3), jb = ja + 1;
+        // int8: snake order (odd rows walk the B tiles backwards, so
+        // consecutive MFMAs always share an operand; config-3 int8 +0.3 %,
+        // four interleaved pairs, none slower). The 16-bit types keep the
+        // plain order. Every accumulator's k order is the same either way.
+        constexpr bool kSnake = std::is_same<Op, OpI8>::value;
+        const bool rev = kSnake && (i & 1) != 0;
+        const int ja = rev ? 7 - 2 * (q & 3) : 2 * (q & 3);
+        const int jb = rev ? ja - 1 : ja + 1;
         if ((q + 1) * cnt / 32 > q * cnt / 32) dma_d(dma_kt, dma_st, d0 + q * cnt / 32, full);
         __builtin_amdgcn_sched_barrier(0);
         Op::mma16(fa[i], fb[buf][ja], acc[i][ja]);
