@@ -177,9 +177,9 @@ grxblasStatus_t grxblasGetTensorTypes(grxblasHandle_t handle,
 grxblasStatus_t grxblasSetTensorMapSlots(grxblasHandle_t handle,
                                          int slotA, int slotB);
 
-/* The matrix-core instruction tile GemmEx is built from (ref grxblas.h:
- * 142-143): 32 x 32 x 16 for fp16/bf16 (v_mfma_f32_32x32x16_*). The int8
- * instruction is 32 x 32 x 32. */
+/* The matrix-core instruction tile GemmEx's main (T,N) path is built from
+ * (ref grxblas.h:142-143): 16 x 16 x 32 for fp16/bf16
+ * (v_mfma_f32_16x16x32_*); int8 uses 16 x 16 x 64. */
 grxblasStatus_t grxblasGetTensorTile(grxblasHandle_t handle,
                                      int* m, int* n, int* k);
 

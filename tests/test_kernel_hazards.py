@@ -1,8 +1,8 @@
 """gfx950 wait-state rules checked on the built kernels' assembly (CPU).
 
-The kernels issue some instructions as inline assembly (the attention P.V
-MFMAs with AGPR accumulators, the direct-to-LDS buffer loads of attention and
-gemm_tn128). The compiler's hazard recognizer does not look inside inline
+The kernels issue some instructions as inline assembly (gemm_tn_fast's
+16x16 MFMAs, which accumulate in place in AGPRs, and the direct-to-LDS buffer
+loads of attention and gemm_tn128). The compiler's hazard recognizer does not look inside inline
 assembly, so those statements carry their own s_nop, and this test checks
 the result on the code the build produces: every kernel source is compiled
 to gfx950 assembly with the build's own flags, and the instruction stream of
