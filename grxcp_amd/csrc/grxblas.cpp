@@ -410,9 +410,9 @@ grxblasStatus_t grxblasGetTensorTile(grxblasHandle_t handle, int* m, int* n, int
   if (!m || !n || !k) return GRXBLAS_STATUS_INVALID_VALUE;
   const grxblasStatus_t s = ensure_ready(*handle);
   if (s != GRXBLAS_STATUS_SUCCESS) return s;
-  *m = 16;
-  *n = 16;
-  *k = 32;
+  *m = 32;
+  *n = 32;
+  *k = 16;
   return GRXBLAS_STATUS_SUCCESS;
 }
 

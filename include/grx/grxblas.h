@@ -177,9 +177,11 @@ grxblasStatus_t grxblasGetTensorTypes(grxblasHandle_t handle,
 grxblasStatus_t grxblasSetTensorMapSlots(grxblasHandle_t handle,
                                          int slotA, int slotB);
 
-/* The matrix-core instruction tile GemmEx's main (T,N) path is built from
- * (ref grxblas.h:142-143): 16 x 16 x 32 for fp16/bf16
- * (v_mfma_f32_16x16x32_*); int8 uses 16 x 16 x 64. */
+/* The matrix-core tile one wavefront computes per instruction on GemmEx's
+ * general path, the one every layout and small shape takes (ref grxblas.h:
+ * 142-143): 32 x 32 x 16 for fp16/bf16 (v_mfma_f32_32x32x16_*; int8
+ * 32 x 32 x 32). The (T,N) path of large problems runs 16 x 16 x 32
+ * instructions (int8 16 x 16 x 64), eight by eight per wavefront. */
 grxblasStatus_t grxblasGetTensorTile(grxblasHandle_t handle,
                                      int* m, int* n, int* k);
 

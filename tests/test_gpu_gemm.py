@@ -106,7 +106,7 @@ def test_tensor_tile_and_types(blas):
     import ctypes
     m, n, k, t = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_uint()
     assert blas.L.grxblasGetTensorTile(blas.h, ctypes.byref(m), ctypes.byref(n), ctypes.byref(k)) == 0
-    assert (m.value, n.value, k.value) == (16, 16, 32)
+    assert (m.value, n.value, k.value) == (32, 32, 16)
     assert blas.L.grxblasGetTensorTypes(blas.h, ctypes.byref(t)) == 0
     assert t.value & g.TENSOR_FP16 and t.value & g.TENSOR_BF16 and t.value & g.TENSOR_INT8
     p = ctypes.c_char_p()
