@@ -1235,6 +1235,7 @@ bool tn_ready(const GemmDesc& d) {
 // reduce_splits applies the epilogue to their sum. Workspace layout: copy of
 // A, copy of B, partials, each 256-byte aligned.
 constexpr int kSplitTiles = 256;
+constexpr int kTn128Tiles = 96;   // gemm_tn128 below this many 256x256 tiles
 constexpr int kMaxSplit = 16;
 constexpr int64_t kFixNs = 8000, kStageNs = 1030, kReduceNs = 6000, kPartialBytesPerNs = 10000;
 // An fp32 stage (32 elements of K) is 8x the MFMA work of a 16-bit one; measured
@@ -1317,11 +1318,15 @@ Plan make_plan(const GemmDesc& d) {
   constexpr bool kF32 = std::is_same<Op, OpF32>::value;
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
   const int64_t stages = ((int64_t)d.k * EB + kFastKBytes - 1) / kFastKBytes;
-  // 16-bit and int8 problems of at least 1024 x 1024 with few 256x256 tiles
-  // and at most 32 stages of K: 128x128 tiles, one pass (2048^3 bf16: 470 ->
-  // 520 TFLOP/s against 3 slices; 1024^3 94 -> 111). Longer K keeps the
-  // 256x256 kernel (3072^3: 1026 against 574 on 128x128 tiles).
-  if (!kF32 && tiles < kSplitTiles && stages <= 32 && d.m >= 1024 && d.n >= 1024) {
+  // 16-bit and int8 problems of at least 1024 x 1024 with fewer than 96
+  // tiles of 256x256 and at most 32 stages of K: 128x128 tiles, one pass
+  // (2048^3 bf16: 510 TFLOP/s against 460 in 3 slices of 256x256 tiles;
+  // 1024^3 113 against 89). From 96 tiles on the 256x256 kernel's 16x16
+  // tiles win (bf16, K = 1024 / 2048: 96 tiles 499 / 625 against 389 / 554
+  // on 128x128 tiles, 128 tiles 661 / 801 against 468 / 659, 144 tiles 730 /
+  // 879 against 368 / 515). Longer K keeps the 256x256 kernel (3072^3: 1026
+  // against 574 on 128x128 tiles).
+  if (!kF32 && tiles < kTn128Tiles && stages <= 32 && d.m >= 1024 && d.n >= 1024) {
     t.tn128 = true;
     return t;
   }
