@@ -495,24 +495,6 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
     const int rcol = lane / kLanesPerCol;
     const int run_pos = run * kRun + 4 * ((run * kRun >> 6) & 1);
     const int gi = row0 + wm * 128 + run * kRun;
-    // Dequant: the 32 column scales this lane applies (4 column blocks x the
-    // 32 / kColsPerRound runs of each), loaded together as the epilogue
-    // starts so their latency overlaps the first block's LDS round trip,
-    // instead of one dependent load per run (config-3 int8: the epilogue took
-    // 15.6K cycles per tile against bf16's 9.7K for the same output; +0.8 %
-    // end to end, bit-identical).
-    constexpr bool kDeq = OUT == MmaOut::DEQ_BF16;
-    constexpr int kRunsPerBlock = 32 / kColsPerRound;
-    float dscale[kDeq ? 4 : 1][kDeq ? kRunsPerBlock : 1];
-    if constexpr (kDeq) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int rd = 0; rd < kRunsPerBlock; ++rd) {
-          const int gj = col0 + wn * 128 + 32 * j + rd * kColsPerRound + rcol;
-          dscale[j][rd] = gj < p.n ? p.scale[gj] : 0.0f;
-        }
-    }
     // One column block per call; J is a compile-time constant so that the
     // accumulators stay in registers (a run-time index would move them to
     // scratch).
@@ -541,10 +523,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
           const int col = rd * kColsPerRound + rcol;
           E v[kRun];
           read_run(col, v);
-          if constexpr (kDeq)
-            Epi<OUT>::template put_run_scaled<STREAM>(cbase + (int64_t)col * p.ldc, v, dscale[j][rd]);
-          else
-            Epi<OUT>::template put_run<STREAM>(p, cbase + (int64_t)col * p.ldc, v, gj0 + col);
+          Epi<OUT>::template put_run<STREAM>(p, cbase + (int64_t)col * p.ldc, v, gj0 + col);
         }
       } else {
         for (int rd = 0; rd < 32 / kColsPerRound; ++rd) {
@@ -692,18 +671,98 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
     __syncthreads();                                     // and no wave still reads a stage
 
     // Lane l holds rows 16i + 4*(l/16) .. +3 of column 16*jj + l%16.
-    epilogue([&](auto jc) __attribute__((always_inline)) {
-      constexpr int j = decltype(jc)::value;
+    if constexpr (OUT == MmaOut::DEQ_BF16) {
+      // Dequantised int8: each value is scaled and rounded to bf16 in
+      // registers (the same correctly rounded operations as
+      // Epi<DEQ_BF16>::put_run_scaled, so the bits are unchanged) before it
+      // is parked, and the LDS round trip moves half the bytes of the
+      // 32-bit form: config-3 int8 2945 -> 2975 TOP/s (+1.0 %, six runs of
+      // each in ABBA order, one box). The same for 16-bit C at beta = 0
+      // measured -0.2 % (bf16 8192^3) and -0.5 % (4096^3), so those keep
+      // the 32-bit park.
+      // Per wave, a 128x32 column block at a time: [col][row] bf16, 68
+      // words per column. A lane parks 4 rows (8 bytes) of one column per
+      // 16x16 tile: the 32 lanes of a ds_write_b64 cycle put columns on
+      // banks 4*c and their 4 words beside them, all 64 banks once. Read
+      // back as runs of 8 rows (16 bytes), 16 lanes per column: one
+      // column's 64 consecutive words per ds_read_b128 cycle.
+      {
+        constexpr int kPitchH = 64 + 4;
+        uint32_t* sh = (uint32_t*)&lds[0][0][0] + wave * 32 * kPitchH;   // 8.5 KB per wave
+        const int run = lane & 15;
+        const int rcol = lane >> 4;
+        const int gr0 = row0 + wm * 128;
+        const bool rows_full = gr0 + 128 <= p.m;
+        // The 8 column scales this lane parks, loaded together.
+        float dsc[4][2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          i32x4 w;
+          for (int h = 0; h < 2; ++h) {
+            const int gj = col0 + wn * 128 + 32 * j + 16 * h + r16;
+            dsc[j][h] = gj < p.n ? p.scale[gj] : 0.0f;
+          }
+        auto narrow2 = [&](int a, int b, float s) __attribute__((always_inline)) -> uint32_t {
+          return pack_bf16x2(__fmul_rn((float)a, s), __fmul_rn((float)b, s));
+        };
+        auto column_block16 = [&](auto jc) __attribute__((always_inline)) {
+          constexpr int j = decltype(jc)::value;
+          // This block's accumulators are read only from here on: without
+          // the fence the compiler converts later blocks early and spills.
 #pragma unroll
-          for (int q = 0; q < 4; ++q) w[q] = bits_of(acc[i][2 * j + h][q]);
-          *(i32x4*)&stage[(16 * h + r16) * kPitch + 16 * i + 4 * (lane >> 4) + 4 * (i >> 2)] = w;
-        }
-    });
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) asm volatile("" : "+a"(acc[i][2 * j + h]));
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const auto& a = acc[i][2 * j + h];
+              u32x2 w;
+              w[0] = narrow2(a[0], a[1], dsc[j][h]);
+              w[1] = narrow2(a[2], a[3], dsc[j][h]);
+              *(u32x2*)&sh[(16 * h + r16) * kPitchH + 8 * i + 2 * (lane >> 4)] = w;
+            }
+          asm volatile("" ::: "memory");
+          const int gj0 = col0 + wn * 128 + 32 * j;
+          uint16_t* cb = (uint16_t*)p.c + (int64_t)gj0 * p.ldc + gr0 + 8 * run;
+          if (rows_full && gj0 + 32 <= p.n) {
+#pragma unroll
+            for (int rd = 0; rd < 8; ++rd) {
+              const int col = 4 * rd + rcol;
+              put16<STREAM>(cb + (int64_t)col * p.ldc, *(const u32x4*)&sh[col * kPitchH + 4 * run]);
+            }
+          } else {
+            for (int rd = 0; rd < 8; ++rd) {
+              const int col = 4 * rd + rcol;
+              const u32x4 w = *(const u32x4*)&sh[col * kPitchH + 4 * run];
+              if (gj0 + col >= p.n) continue;
+              for (int q = 0; q < 8; ++q)
+                if (gr0 + 8 * run + q < p.m)
+                  cb[(int64_t)col * p.ldc + q] = (uint16_t)(w[q >> 1] >> (16 * (q & 1)));
+            }
+          }
+          asm volatile("" ::: "memory");
+        };
+        column_block16(IntC<0>{});
+        column_block16(IntC<1>{});
+        column_block16(IntC<2>{});
+        column_block16(IntC<3>{});
+      }
+    } else {
+      epilogue([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            i32x4 w;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[q] = bits_of(acc[i][2 * j + h][q]);
+            *(i32x4*)&stage[(16 * h + r16) * kPitch + 16 * i + 4 * (lane >> 4) + 4 * (i >> 2)] = w;
+          }
+      });
+    }
   } else {
     // fp32: 4 x 4 tiles of 32x32 per wave, 32-byte k-steps (four per stage).
     using Acc = typename Op::Acc;
