@@ -907,19 +907,27 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
 // ---------------------------------------------------------------------------
 
 // For 16-bit and int8 TN problems with few 256x256 tiles and short K, where
-// neither one pass of gemm_tn_fast nor a split fills the GPU cheaply: 4 waves
-// of 64x64 (2x2 MFMA tiles each) per 128x128 tile, gemm_tn_fast's stage
-// layout and swizzle at half the rows (64 KB of LDS, two workgroups per CU),
-// a double-buffered K loop, C stored from registers in runs of 4 rows. The
-// DMA is issued as inline assembly: through the builtin, the compiler's
-// wait-count pass cannot tell the stage reads from the DMA still landing in
-// the other buffer and waits for all of it before every barrier.
+// neither one pass of gemm_tn_fast nor a split fills the GPU cheaply. One
+// workgroup per CU, 4 waves of 64x64 per 128x128 tile, each wave 4 x 4 tiles
+// of 16x16 MFMAs accumulated in place in AGPRs (gemm_tn_fast's assembly
+// MFMA, fragment chunk order and stage swizzle at half the rows). K streams
+// through a ring of four 128-byte LDS stages (128 KB): three stages are in
+// flight while one is read, so a load has three stages of MFMA time to
+// land, and one barrier per stage both publishes the next stage and frees
+// the one the DMA refills. Fragments are double-buffered one k-step ahead,
+// read between the MFMAs. The DMA is issued as inline assembly: through the
+// builtin, the compiler's wait-count pass cannot tell the stage reads from
+// the DMA still landing in the other stages and waits for all of it before
+// every barrier. C is stored from registers, 4 rows of one column per lane
+// (8 or 16 bytes).
 constexpr int kT128 = 128;
 
 template <class Op, MmaOut OUT>
-__global__ __launch_bounds__(256, 2) void gemm_tn128(KParams batch_p) {
-  constexpr int NS = 2;
+__global__ __launch_bounds__(256, 1) void gemm_tn128(KParams batch_p) {
+  constexpr int NS = 4;                                   // stages in the ring
+  constexpr uint32_t kStage = kT128 * kChunks * 16;       // 16 KB per operand and stage
   const KParams p = batch_view(batch_p);
+  // [A | B][stage][row * 8 + physical chunk], 16 bytes per entry.
   __shared__ __attribute__((aligned(1024))) i32x4 lds[2][NS][kT128 * kChunks];
   const uint64_t t0 = p.probe ? cycle_now() : 0;
   const int tid = threadIdx.x;
@@ -934,7 +942,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tn128(KParams batch_p) {
   const int ktiles = (kbytes + kFastKBytes - 1) / kFastKBytes;
   // Buffer descriptors as in gemm_tn_fast (record count ending at row m or
   // n, so rows past the matrix read zero; offset 2^31 reads zero for a
-  // masked k chunk), as the four words the assembly takes.
+  // masked k chunk or a stage past K), as the four words the assembly takes.
   const int rows_a = min(kT128, p.m - row0);
   const int rows_b = min(kT128, p.n - col0);
   constexpr uint32_t kOff = 0x80000000u;
@@ -949,6 +957,9 @@ __global__ __launch_bounds__(256, 2) void gemm_tn128(KParams batch_p) {
   };
   const i32x4 rsa = rsrc_words(p.a + (int64_t)row0 * lda_b, (rows_a - 1) * lda_b + kbytes);
   const i32x4 rsb = rsrc_words(p.b + (int64_t)col0 * ldb_b, (rows_b - 1) * ldb_b + kbytes);
+  // DMA instruction d (0..7) of a stage: operand d / 4, the 1 KB block of
+  // rows 8*(4*(d%4) + wave) .. +7, lane L landing in row +L/8 at physical
+  // chunk L%8 and fetching logical chunk (L%8) ^ swz(row).
   const int lr = lane >> 3, pc = lane & 7;
   uint32_t base_a[4], base_b[4];
 #pragma unroll
@@ -959,91 +970,139 @@ __global__ __launch_bounds__(256, 2) void gemm_tn128(KParams batch_p) {
     base_a[i] = (uint32_t)(row * lda_b + 16 * c);
     base_b[i] = (uint32_t)(row * ldb_b + 16 * c);
   }
-  auto dma = [&](int kt, int st) {
+  auto dma = [&](int kt, int st, int d) __attribute__((always_inline)) {
+    const int i = d & 3;
+    const int blk = 4 * i + wave;
     const int kb = kt * kFastKBytes;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int blk = 4 * i + wave;
-      const int c = pc ^ lr ^ (blk & 7);
-      const bool ok = kb + 16 * c < kbytes;
-      const uint32_t va = ok ? base_a[i] + (uint32_t)kb : kOff;
-      const uint32_t vb = ok ? base_b[i] + (uint32_t)kb : kOff;
-      const uint32_t la = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][st][blk * 64];
-      const uint32_t lb = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[1][st][blk * 64];
-      // One wait state between the M0 write and the DMA that reads it (the
-      // hazard pass does not look inside inline assembly).
+    const int c = pc ^ lr ^ (blk & 7);
+    const bool ok = kt < ktiles && kb + 16 * c < kbytes;
+    // One wait state between the M0 write and the DMA that reads it (the
+    // hazard pass does not look inside inline assembly).
+    if (d < 4) {
+      const uint32_t v = ok ? base_a[i] + (uint32_t)kb : kOff;
+      const uint32_t l = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][st][blk * 64];
       asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                   :: "s"(la), "v"(va), "s"(rsa) : "memory");
+                   :: "s"(l), "v"(v), "s"(rsa) : "memory");
+    } else {
+      const uint32_t v = ok ? base_b[i] + (uint32_t)kb : kOff;
+      const uint32_t l = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[1][st][blk * 64];
       asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                   :: "s"(lb), "v"(vb), "s"(rsb) : "memory");
+                   :: "s"(l), "v"(v), "s"(rsb) : "memory");
     }
   };
-  using Acc = typename Op::Acc;
-  Acc acc[2][2];
+
+  using Acc = typename Op::Acc16;
+  Acc acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-  const int wm = wave >> 1, wn = wave & 1, r32 = lane & 31, hh = lane >> 5;
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0;
+  const int wm = wave >> 1, wn = wave & 1, r16 = lane & 15;
+  // Chunks of a 64-byte k-step to the four 16-lane groups in the order
+  // 0, 2, 1, 3 (A and B alike), as in gemm_tn_fast: conflict-free reads.
+  const int kq = ((lane >> 3) & 2) | ((lane >> 5) & 1);
+  typedef __attribute__((address_space(3))) const i32x4* lds_frag_t;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][0][0];
+  uint32_t ad_a[4][2], ad_b[4][2];                        // stage 0, [tile][k-step]
 #pragma unroll
-  for (int q = 0; q < NS - 1; ++q)
-    if (q < ktiles) dma(q, q);
-  int st = 0;
-  for (int kt = 0; kt < ktiles; ++kt) {
-    // stage kt+NS-1 is issued at the top so NS-1 stages are in flight
-    if (kt + NS - 1 < ktiles) {
-      int stn = st + NS - 1; if (stn >= NS) stn -= NS;
-      dma(kt + NS - 1, stn);
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int kc = 4 * ks + kq;
+      const int ar = wm * 64 + 16 * t + r16;
+      const int br = wn * 64 + 16 * t + r16;
+      ad_a[t][ks] = lds0 + 16u * (uint32_t)(ar * kChunks + (kc ^ swz(ar)));
+      ad_b[t][ks] = lds0 + NS * kStage + 16u * (uint32_t)(br * kChunks + (kc ^ swz(br)));
     }
-    const int ahead = min(ktiles - 1 - kt, NS - 1);    // stages issued after kt
-    if (ahead >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    i32x4 fa[2][2], fb[2][2];
-    auto rd = [&](int ks, int b) {
+  i32x4 fa[2][4], fb[2][4];
+  // One k-step: 16 MFMAs (A tile q/4 x B tile q%4). Behind the odd slots,
+  // the next k-step's 8 fragments (stage offset `off`, k-step `rks`) into
+  // the other register set; ahead of the even slots, DMA instruction q/2
+  // of stage `dkt` into ring slot `dst` when `dma_on`.
+  auto kstep = [&](auto bufc, uint32_t off, int rks, bool dma_on, int dkt, int dst)
+      __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int ar = wm * 64 + 32 * t + r32;
-        const int br = wn * 64 + 32 * t + r32;
-        typedef __attribute__((address_space(3))) const i32x4* lds_frag_t;
-        const uint32_t l0 = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][0][0];
-        const uint32_t oa = 16u * (uint32_t)((0 * NS + st) * kT128 * kChunks + ar * kChunks + ((2 * ks + hh) ^ swz(ar)));
-        const uint32_t ob = 16u * (uint32_t)((1 * NS + st) * kT128 * kChunks + br * kChunks + ((2 * ks + hh) ^ swz(br)));
-        fa[b][t] = *(lds_frag_t)(uintptr_t)(l0 + oa);
-        fb[b][t] = *(lds_frag_t)(uintptr_t)(l0 + ob);
+    for (int q = 0; q < 16; ++q) {
+      if (dma_on && (q & 1) == 0) dma(dkt, dst, q >> 1);
+      __builtin_amdgcn_sched_barrier(0);
+      Op::mma16(fa[buf][q >> 2], fb[buf][q & 3], acc[q >> 2][q & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q & 1) {
+        const int f = q >> 1;
+        if (f < 4) fa[buf ^ 1][f] = *(lds_frag_t)(uintptr_t)(ad_a[f][rks] + off);
+        else fb[buf ^ 1][f - 4] = *(lds_frag_t)(uintptr_t)(ad_b[f - 4][rks] + off);
       }
-    };
-    rd(0, 0);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (ks + 1 < 4) rd(ks + 1, (ks + 1) & 1);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
-    st = st + 1 == NS ? 0 : st + 1;
+  };
+
+  // Stages 0 .. NS-1 in flight, then stage 0 landed. Stage s lives in ring
+  // slot s % NS; a stage past K is a zero fill, so every stage issues the
+  // same 8 DMA instructions per wave and the waits below count uniformly.
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) dma(s, s, d);
+  asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    fa[0][t] = *(lds_frag_t)(uintptr_t)ad_a[t][0];
+    fb[0][t] = *(lds_frag_t)(uintptr_t)ad_b[t][0];
   }
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int st = kt & (NS - 1);
+    // k-step 0 of stage kt; its k-step 1 fragments read alongside
+    kstep(IntC<0>{}, (uint32_t)st * kStage, 1, false, 0, 0);
+    // Stage kt+1 landed (stages kt+2, kt+3 may still be in flight), and no
+    // wave reads stage kt any more: its slot takes stage kt+NS.
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    __syncthreads();
+    kstep(IntC<1>{}, (uint32_t)((kt + 1) & (NS - 1)) * kStage, 0, true, kt + NS, st);
+  }
+  // The MFMAs are assembly, so the compiler places the epilogue's reads of
+  // their results without knowing what wrote them: 18 wait states first.
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // no LDS write may outlive the workgroup
+
+  // Lane l holds rows 16i + 4*(l/16) .. +3 of column 16j + l%16.
   using E = typename Op::Elem;
+  using T = typename Epi<OUT>::T;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int gj = col0 + wn * 64 + 32 * j + r32;
-      if (gj >= p.n) continue;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int i0 = row0 + wm * 64 + 32 * i + 8 * g + 4 * hh;
-        if (i0 >= p.m) continue;
-        const E v[4] = {(E)acc[i][j][4 * g], (E)acc[i][j][4 * g + 1], (E)acc[i][j][4 * g + 2],
-                        (E)acc[i][j][4 * g + 3]};
-        store_run<OUT>(p, i0, gj, v, 4, Epi<OUT>::kRun == 4);
+    for (int j = 0; j < 4; ++j) {
+      const int gj = col0 + wn * 64 + 16 * j + r16;
+      const int i0 = row0 + wm * 64 + 16 * i + 4 * (lane >> 4);
+      if (gj >= p.n || i0 >= p.m) continue;
+      const E v[4] = {(E)acc[i][j][0], (E)acc[i][j][1], (E)acc[i][j][2], (E)acc[i][j][3]};
+      if constexpr (Epi<OUT>::kRun == 4) {
+        store_run<OUT>(p, i0, gj, v, 4, true);
+      } else if (i0 + 4 <= p.m) {
+        // 16-bit C: the run's 8 bytes, each value as Epi<OUT>::put_run
+        // (or put_run_scaled) rounds it.
+        T* c = (T*)p.c + (int64_t)gj * p.ldc + i0;
+        u32x2 o;
+        if constexpr (OUT == MmaOut::DEQ_BF16) {
+          const float s = p.scale[gj];
+          o[0] = pack_bf16x2(__fmul_rn((float)v[0], s), __fmul_rn((float)v[1], s));
+          o[1] = pack_bf16x2(__fmul_rn((float)v[2], s), __fmul_rn((float)v[3], s));
+        } else if (p.beta == 0.0f) {
+          o[0] = Epi<OUT>::pack(__fmul_rn(p.alpha, v[0]), __fmul_rn(p.alpha, v[1]));
+          o[1] = Epi<OUT>::pack(__fmul_rn(p.alpha, v[2]), __fmul_rn(p.alpha, v[3]));
+        } else {
+          const u32x2 old = *(const u32x2*)c;
+          o[0] = Epi<OUT>::pack(Epi<OUT>::apply(p, v[0], (uint16_t)(old[0] & 0xffff)),
+                                Epi<OUT>::apply(p, v[1], (uint16_t)(old[0] >> 16)));
+          o[1] = Epi<OUT>::pack(Epi<OUT>::apply(p, v[2], (uint16_t)(old[1] & 0xffff)),
+                                Epi<OUT>::apply(p, v[3], (uint16_t)(old[1] >> 16)));
+        }
+        *(u32x2*)c = o;
+      } else {
+        store_run<OUT>(p, i0, gj, v, 4, false);
       }
     }
   cycle_record(p.probe, t0, probe_slot(wave), wave);
@@ -1294,7 +1353,7 @@ bool tn_ready(const GemmDesc& d) {
 // reduce_splits applies the epilogue to their sum. Workspace layout: copy of
 // A, copy of B, partials, each 256-byte aligned.
 constexpr int kSplitTiles = 256;
-constexpr int kTn128Tiles = 96;   // gemm_tn128 below this many 256x256 tiles
+constexpr int kTn128MaxTiles = 256;   // gemm_tn128 up to this many 128x128 tiles
 constexpr int kMaxSplit = 16;
 constexpr int64_t kFixNs = 8000, kStageNs = 1030, kReduceNs = 6000, kPartialBytesPerNs = 10000;
 // An fp32 stage (32 elements of K) is 8x the MFMA work of a 16-bit one; measured
@@ -1377,15 +1436,20 @@ Plan make_plan(const GemmDesc& d) {
   constexpr bool kF32 = std::is_same<Op, OpF32>::value;
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
   const int64_t stages = ((int64_t)d.k * EB + kFastKBytes - 1) / kFastKBytes;
-  // 16-bit and int8 problems of at least 1024 x 1024 with fewer than 96
-  // tiles of 256x256 and at most 32 stages of K: 128x128 tiles, one pass
-  // (2048^3 bf16: 510 TFLOP/s against 460 in 3 slices of 256x256 tiles;
-  // 1024^3 113 against 89). From 96 tiles on the 256x256 kernel's 16x16
-  // tiles win (bf16, K = 1024 / 2048: 96 tiles 499 / 625 against 389 / 554
-  // on 128x128 tiles, 128 tiles 661 / 801 against 468 / 659, 144 tiles 730 /
-  // 879 against 368 / 515). Longer K keeps the 256x256 kernel (3072^3: 1026
-  // against 574 on 128x128 tiles).
-  if (!kF32 && tiles < kTn128Tiles && stages <= 32 && d.m >= 1024 && d.n >= 1024) {
+  // 16-bit and int8 problems whose 128x128 tiles fit one pass over the CUs
+  // (at most 256) run on 128x128 tiles unless K is long against the tile
+  // count: up to 32 stages always, beyond that while 25 * stages <= 16 *
+  // tiles; the rest keep the 256x256 kernel, split or not. Measured (bf16
+  // TFLOP/s, 128x128 kernel against the alternative, same runs): 1024^3 170
+  // / 89, 2048^3 706 / 462, 768^3 85 / 45, 1024^2 x 2048 214 / 162;
+  // 1536^2 x 4096 (144 tiles, 64 stages) 540 / 464, 2048^2 x 4096 839 /
+  // 674, 1280^2 x 4096 (100, 64) 384 / 353, 768 x 2048 x 4096 (96, 64) 372
+  // / 384, 1024^2 x 3072 (64, 48) 237 / 240, 2048 x 1024 x 8192 (128, 128)
+  // 544 / 676, 2048^2 x 8192 (256, 128) 967 / 963; past 256 tiles the
+  // 256x256 kernel ties or wins (2304^2 x 2048 530 / 527, 2048 x 4096 x
+  // 1024 616 / 640, 4096^2 x 1024 671 / 1057).
+  const int64_t tiles128 = (int64_t)((d.m + kT128 - 1) / kT128) * ((d.n + kT128 - 1) / kT128);
+  if (!kF32 && tiles128 <= kTn128MaxTiles && (stages <= 32 || 25 * stages <= 16 * tiles128)) {
     t.tn128 = true;
     return t;
   }
@@ -1523,7 +1587,10 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   } else if (t.tn && t.tn128) {
     p.tiles_m = (g->m + kT128 - 1) / kT128;
     p.tiles_n = (g->n + kT128 - 1) / kT128;
-    hipLaunchKernelGGL((gemm_tn128<Op, OUT>), dim3(p.tiles_m * p.tiles_n, g->batch), dim3(256), 0, s, p);
+    if constexpr (Op::kM16)   // the plan takes this path for 16-bit and int8 inputs only
+      hipLaunchKernelGGL((gemm_tn128<Op, OUT>), dim3(p.tiles_m * p.tiles_n, g->batch), dim3(256), 0, s, p);
+    else
+      return hipErrorInvalidValue;
   } else if (t.tn) {
     p.tiles_m = (g->m + kFastTile - 1) / kFastTile;
     p.tiles_n = (g->n + kFastTile - 1) / kFastTile;

@@ -194,7 +194,7 @@ def test_workspace_grows_and_follows_stream_changes():
 @pytest.mark.parametrize("m,n,k,alpha,beta,pad,cpad", [
     (1024, 1024, 8192, 1.0, 0.0, 0, 0),      # 16 tiles, 128 stages
     (300, 520, 4160, 2.5, -1.5, 8, 4),       # ragged m/n, last slice shorter
-    (512, 2048, 2048, 1.0, 0.0, 0, 8),       # 16 tiles, 32 stages
+    (512, 2048, 4096, 1.0, 0.0, 0, 8),       # 16 tiles, 64 stages
 ])
 def test_split_k_exact(blas, capfd, in_t, out_t, m, n, k, alpha, beta, pad, cpad):
     """Problems with few 256x256 tiles and a long K are split along K; the

@@ -49,11 +49,11 @@ def plant_specials(A: np.ndarray, B: np.ndarray, in_t: int) -> tuple[np.ndarray,
 
 @pytest.mark.parametrize("in_t,out_t", [(BF16, F32), (BF16, BF16), (F16, F32), (F16, F16)])
 @pytest.mark.parametrize("name,ta,tb,m,n,k,kernel,split", [
-    ("tn256", 1, 0, 256, 256, 128, "tn256", False),
+    ("tn256", 1, 0, 2304, 2304, 64, "tn256", False),     # over 256 tiles of 128x128
     ("general64", 1, 0, 37, 29, 45, "general64", False),
-    ("split K", 1, 0, 512, 2048, 2048, "tn256", True),
+    ("split K", 1, 0, 512, 2048, 4096, "tn256", True),
     ("tn128", 1, 0, 1032, 1100, 200, "tn128", False),
-    ("operand copy (N,N)", 0, 0, 320, 264, 512, "tn256", False),
+    ("operand copy (N,N)", 0, 0, 320, 264, 512, "tn128", False),
 ])
 def test_gemm_ex_specials_and_subnormals(blas, capfd, in_t, out_t, name, ta, tb, m, n, k, kernel, split):
     st = O.HalvesStream(m + n + k)

@@ -42,8 +42,8 @@ def _shape(r, kind, elem_bytes):
     # and m*n*k >= 2^25 so that other layouts take the transposed copies
     m = 8 * int(r.integers(40, 96))
     n = int(r.integers(300, 768))
-    if kind == "split":                         # few tiles, K of 16 to 65 stages
-        k = unit * int(r.integers(2048 // unit, 4160 // unit))
+    if kind == "split":                         # few tiles, K of 32 to 65 stages
+        k = unit * int(r.integers(4096 // 16, 8320 // 16))
     else:                                       # a layout other than (T, N), one pass
         ta, tb = _pick(r, [(0, 0), (0, 1), (1, 1)])
         k = unit * int(r.integers(512 // unit, 1008 // unit))
@@ -54,7 +54,7 @@ def _covered(plans):
     return {"split": any(int(p["split"]) > 1 for p in plans),
             "copy_a": any(p["copy_a"] == "1" for p in plans),
             "copy_b": any(p["copy_b"] == "1" for p in plans),
-            "tn256 one pass": any(p["kernel"] == "tn256" and p["split"] == "1" for p in plans),
+            "tn128": any(p["kernel"] == "tn128" for p in plans),
             "general64": any(p["kernel"] == "general64" for p in plans)}
 
 
