@@ -922,9 +922,9 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
 // (8 or 16 bytes).
 constexpr int kT128 = 128;
 
-template <class Op, MmaOut OUT>
-__global__ __launch_bounds__(256, 1) void gemm_tn128(KParams batch_p) {
-  constexpr int NS = 4;                                   // stages in the ring
+template <class Op, MmaOut OUT, int NS>
+__global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch_p) {
+  static_assert(NS == 2 || NS == 4, "stages in the ring: 4 (one workgroup per CU) or 2 (two)");
   constexpr uint32_t kStage = kT128 * kChunks * 16;       // 16 KB per operand and stage
   const KParams p = batch_view(batch_p);
   // [A | B][stage][row * 8 + physical chunk], 16 bytes per entry.
@@ -1046,7 +1046,8 @@ __global__ __launch_bounds__(256, 1) void gemm_tn128(KParams batch_p) {
   for (int s = 0; s < NS; ++s)
 #pragma unroll
     for (int d = 0; d < 8; ++d) dma(s, s, d);
-  asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  if constexpr (NS == 4) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -1059,7 +1060,8 @@ __global__ __launch_bounds__(256, 1) void gemm_tn128(KParams batch_p) {
     kstep(IntC<0>{}, (uint32_t)st * kStage, 1, false, 0, 0);
     // Stage kt+1 landed (stages kt+2, kt+3 may still be in flight), and no
     // wave reads stage kt any more: its slot takes stage kt+NS.
-    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    if constexpr (NS == 4) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     kstep(IntC<1>{}, (uint32_t)((kt + 1) & (NS - 1)) * kStage, 0, true, kt + NS, st);
   }
@@ -1353,7 +1355,7 @@ bool tn_ready(const GemmDesc& d) {
 // reduce_splits applies the epilogue to their sum. Workspace layout: copy of
 // A, copy of B, partials, each 256-byte aligned.
 constexpr int kSplitTiles = 256;
-constexpr int kTn128MaxTiles = 256;   // gemm_tn128 up to this many 128x128 tiles
+constexpr int kTn128MaxTiles = 256;   // gemm_tn128's four-stage ring up to this many 128x128 tiles, two-stage up to twice it
 constexpr int kMaxSplit = 16;
 constexpr int64_t kFixNs = 8000, kStageNs = 1030, kReduceNs = 6000, kPartialBytesPerNs = 10000;
 // An fp32 stage (32 elements of K) is 8x the MFMA work of a 16-bit one; measured
@@ -1371,6 +1373,7 @@ struct Plan {
   bool tn = false;                // the TN kernel runs (directly or on copies)
   int64_t split_ns = 0;           // the split's modelled time (fp32 problems of 256+ tiles)
   bool tn128 = false;             // the TN problem runs on 128x128 tiles (gemm_tn128)
+  int tn128_stages = 4;           // its LDS ring: 4 stages (one workgroup per CU) or 2 (two)
   GemmDesc e;                     // the TN problem (over the copies; ws unset)
   size_t bytes() const { return a_bytes + b_bytes + w_bytes; }
 };
@@ -1436,21 +1439,27 @@ Plan make_plan(const GemmDesc& d) {
   constexpr bool kF32 = std::is_same<Op, OpF32>::value;
   const int64_t tiles = (int64_t)((d.m + kFastTile - 1) / kFastTile) * ((d.n + kFastTile - 1) / kFastTile);
   const int64_t stages = ((int64_t)d.k * EB + kFastKBytes - 1) / kFastKBytes;
-  // 16-bit and int8 problems whose 128x128 tiles fit one pass over the CUs
-  // (at most 256) run on 128x128 tiles unless K is long against the tile
-  // count: up to 32 stages always, beyond that while 25 * stages <= 16 *
-  // tiles; the rest keep the 256x256 kernel, split or not. Measured (bf16
+  // 16-bit and int8 problems of at most 512 tiles of 128x128 run on them
+  // unless K is long against the tile count: up to 32 stages always, beyond
+  // that while 25 * stages <= 16 * tiles; the rest keep the 256x256 kernel,
+  // split or not. Up to 256 tiles (one pass over the CUs) the kernel's
+  // four-stage ring, one workgroup per CU; up to 512 its two-stage ring, two
+  // workgroups per CU (2304^2 x 2048 669 against 530 on the 256x256 kernel,
+  // 3072 x 2048 x 2048 736 / 625, 4096 x 2048 x 2048 886 / 798, 2048 x 4096
+  // x 4096 1044 / 949; 2048^3 631 against 695 with four stages; past 512
+  // tiles the 256x256 kernel: 3072^2 x 1024 718 against 588). Measured (bf16
   // TFLOP/s, 128x128 kernel against the alternative, same runs): 1024^3 170
   // / 89, 2048^3 706 / 462, 768^3 85 / 45, 1024^2 x 2048 214 / 162;
   // 1536^2 x 4096 (144 tiles, 64 stages) 540 / 464, 2048^2 x 4096 839 /
   // 674, 1280^2 x 4096 (100, 64) 384 / 353, 768 x 2048 x 4096 (96, 64) 372
   // / 384, 1024^2 x 3072 (64, 48) 237 / 240, 2048 x 1024 x 8192 (128, 128)
   // 544 / 676, 2048^2 x 8192 (256, 128) 967 / 963; past 256 tiles the
-  // 256x256 kernel ties or wins (2304^2 x 2048 530 / 527, 2048 x 4096 x
-  // 1024 616 / 640, 4096^2 x 1024 671 / 1057).
+  // four-stage ring ties or loses to the 256x256 kernel (2304^2 x 2048 530 /
+  // 527, 2048 x 4096 x 1024 616 / 640, 4096^2 x 1024 671 / 1057).
   const int64_t tiles128 = (int64_t)((d.m + kT128 - 1) / kT128) * ((d.n + kT128 - 1) / kT128);
-  if (!kF32 && tiles128 <= kTn128MaxTiles && (stages <= 32 || 25 * stages <= 16 * tiles128)) {
+  if (!kF32 && tiles128 <= 2 * kTn128MaxTiles && (stages <= 32 || 25 * stages <= 16 * tiles128)) {
     t.tn128 = true;
+    t.tn128_stages = tiles128 <= kTn128MaxTiles ? 4 : 2;
     return t;
   }
   if ((!kF32 && tiles >= kSplitTiles) || stages < 16) return t;
@@ -1541,9 +1550,10 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   if (log_plans()) {
     std::fprintf(stderr,
                  "grxblas: gemm %s->%s ta=%d tb=%d m=%d n=%d k=%d batch=%d kernel=%s copy_a=%d "
-                 "copy_b=%d split=%d\n",
+                 "copy_b=%d split=%d ring=%d\n",
                  Op::kName, out_name<OUT>(), (int)d.ta, (int)d.tb, d.m, d.n, d.k, d.batch,
-                 t.tn ? (t.tn128 ? "tn128" : "tn256") : "general64", (int)t.copy_a, (int)t.copy_b, t.split);
+                 t.tn ? (t.tn128 ? "tn128" : "tn256") : "general64", (int)t.copy_a, (int)t.copy_b, t.split,
+                 t.tn && t.tn128 ? t.tn128_stages : 0);
   }
 
   KParams p{};
@@ -1588,7 +1598,12 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     p.tiles_m = (g->m + kT128 - 1) / kT128;
     p.tiles_n = (g->n + kT128 - 1) / kT128;
     if constexpr (Op::kM16)   // the plan takes this path for 16-bit and int8 inputs only
-      hipLaunchKernelGGL((gemm_tn128<Op, OUT>), dim3(p.tiles_m * p.tiles_n, g->batch), dim3(256), 0, s, p);
+    {
+      if (t.tn128_stages == 2)
+        hipLaunchKernelGGL((gemm_tn128<Op, OUT, 2>), dim3(p.tiles_m * p.tiles_n, g->batch), dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL((gemm_tn128<Op, OUT, 4>), dim3(p.tiles_m * p.tiles_n, g->batch), dim3(256), 0, s, p);
+    }
     else
       return hipErrorInvalidValue;
   } else if (t.tn) {

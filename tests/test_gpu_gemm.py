@@ -300,6 +300,34 @@ def test_tn128_stage_limits_and_ragged_rows(blas, capfd, kind, it, ot, m, n, k):
     assert len(plans) == 1 and plans[0]["kernel"] == "tn128", plans
 
 
+def test_tn128_two_stage_ring_exact(blas, capfd):
+    """Between 256 and 512 tiles of 128x128 the kernel runs its two-stage LDS
+    ring, two workgroups per CU: 16-bit and fp32 C, int8 and dequant, (T, N)
+    and (N, N) behind the operand copy, ragged m, n and K, bit-exact over
+    the padded C with guard bands; the log must show that ring."""
+    m, n = 2312, 2184                     # 19 x 18 = 342 tiles
+    cases = [("f", 1, 0, BF16, BF16), ("f", 1, 0, F16, F32), ("f", 0, 0, BF16, F32),
+             ("i8", 1, 0, None, None), ("dq", 1, 0, None, None)]
+    bad = []
+    for kind, ta, tb, it, ot in cases:
+        res = []
+        if kind == "f":
+            call = lambda: res.append(float_case(blas, it, ot, ta, tb, m, n, 136, 1.5, -0.5, 0, 8,  # noqa: E731,B023
+                                                 seed=31 + ta, guard=True))
+            ok = (0, 0)
+        elif kind == "i8":
+            call = lambda: res.append(int8_case(blas, ta, tb, m, n, 272, 2.0, 1.0, 0, fill="rand",  # noqa: E731,B023
+                                                seed=33, cpad=0, guard=True))
+            ok = 0
+        else:
+            call = lambda: res.append(dequant_case(blas, ta, tb, m, n, 272, 0, 8, seed=35, guard=True))  # noqa: E731,B023
+            ok = (0, 0)
+        plans = logged_plans(capfd, call)
+        if res != [ok] or len(plans) != 1 or plans[0]["kernel"] != "tn128" or plans[0]["ring"] != "2":
+            bad.append((kind, ta, tb, it, ot, res, plans))
+    assert not bad, bad
+
+
 def test_split_k_workspaces_on_many_streams():
     """Split-K calls rotating over six streams (more than the handle keeps
     workspaces for per device, so workspaces are handed over) with no host

@@ -49,7 +49,7 @@ def plant_specials(A: np.ndarray, B: np.ndarray, in_t: int) -> tuple[np.ndarray,
 
 @pytest.mark.parametrize("in_t,out_t", [(BF16, F32), (BF16, BF16), (F16, F32), (F16, F16)])
 @pytest.mark.parametrize("name,ta,tb,m,n,k,kernel,split", [
-    ("tn256", 1, 0, 2304, 2304, 64, "tn256", False),     # over 256 tiles of 128x128
+    ("tn256", 1, 0, 2944, 2944, 64, "tn256", False),     # over 512 tiles of 128x128
     ("general64", 1, 0, 37, 29, 45, "general64", False),
     ("split K", 1, 0, 512, 2048, 4096, "tn256", True),
     ("tn128", 1, 0, 1032, 1100, 200, "tn128", False),
