@@ -1417,7 +1417,7 @@ Plan make_plan(const GemmDesc& d) {
       t = c;
     }
   }
-  if (!t.tn || d.batch != 1 || d.probe) return t;
+  if (!t.tn || d.probe) return t;
   // Split K where a cost model (times in ns, fitted to kernel traces of
   // 256x256 tiles at up to 256 workgroups) predicts at least 10 % less time.
   // One pass: kFixNs (launch, prologue, epilogue) + kStageNs per 128-byte K
@@ -1456,12 +1456,21 @@ Plan make_plan(const GemmDesc& d) {
   // 544 / 676, 2048^2 x 8192 (256, 128) 967 / 963; past 256 tiles the
   // four-stage ring ties or loses to the 256x256 kernel (2304^2 x 2048 530 /
   // 527, 2048 x 4096 x 1024 616 / 640, 4096^2 x 1024 671 / 1057).
-  const int64_t tiles128 = (int64_t)((d.m + kT128 - 1) / kT128) * ((d.n + kT128 - 1) / kT128);
-  if (!kF32 && tiles128 <= 2 * kTn128MaxTiles && (stages <= 32 || 25 * stages <= 16 * tiles128)) {
+  // Batches of small problems (at most 16 tiles of 128x128 each) count their
+  // workgroups, batch x tiles: bf16 TFLOP/s against the 256x256 kernel,
+  // same runs, 16 x 256^2 x 64 23 / 14.5, 64 x 256^2 x 128 147 / 101, 32 x
+  // 512^2 x 128 210 / 193 (torch bmm 7.4, 60, 115); batches of larger ones
+  // keep the 256x256 kernel (8 x 1024^3 586 against 625, 12 x 768^3 406
+  // against 454 on 128x128 tiles).
+  const int64_t per128 = (int64_t)((d.m + kT128 - 1) / kT128) * ((d.n + kT128 - 1) / kT128);
+  const int64_t tiles128 = per128 * d.batch;
+  if (!kF32 && (d.batch == 1 || per128 <= 16) && tiles128 <= 2 * kTn128MaxTiles &&
+      (stages <= 32 || 25 * stages <= 16 * tiles128)) {
     t.tn128 = true;
     t.tn128_stages = tiles128 <= kTn128MaxTiles ? 4 : 2;
     return t;
   }
+  if (d.batch != 1) return t;                       // split K: one problem only
   if ((!kF32 && tiles >= kSplitTiles) || stages < 16) return t;
   const int64_t min_per = tiles >= kSplitTiles ? 32 : 8;
   const int64_t mn = ((int64_t)d.m + 7) / 8 * 8 * d.n;

@@ -149,6 +149,26 @@ def test_batched_refusals(blas):
                                         0.0, dc.p, F32, 4, 16, 2) == g.INVALID_VALUE  # lda < k
 
 
+def test_batched_runs_the_128_tile_kernel(blas, capfd):
+    """Batches whose 128x128 workgroups number at most 512 (batch x tiles)
+    run on the 128x128-tile kernel, its four-stage ring up to 256 of them and
+    its two-stage ring up to 512: every batch bit-exact, strides packed,
+    broadcast (0) and negative, C gaps untouched; the plan log shows the
+    kernel and the ring."""
+    from test_gpu_gemm import logged_plans
+    cases = [(BF16, BF16, 256, 256, 128, 3, "packed", "zero", "gap", "4"),      # 12 workgroups
+             (F16, F32, 512, 512, 128, 32, "packed", "packed", "packed", "2"),  # 512
+             (I8, I32, 256, 256, 256, 12, "neg", "packed", "gap", "4")]        # 48
+    bad = []
+    for it, ot, m, n, k, batch, am, bm, cm, ring in cases:
+        res = []
+        plans = logged_plans(capfd, lambda: res.append(batched_case(  # noqa: B023
+            blas, it, ot, 1, 0, m, n, k, 1.0, 0.0, batch, am, bm, cm, seed=batch)))
+        if res != [0] or len(plans) != 1 or plans[0]["kernel"] != "tn128" or plans[0]["ring"] != ring:
+            bad.append((it, ot, m, n, k, batch, res, plans))
+    assert not bad, bad
+
+
 def test_batched_probe_capacity(blas):
     """A cycle probe must hold batchCount times one GemmEx's slots."""
     m = n = 256
