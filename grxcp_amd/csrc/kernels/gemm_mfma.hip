@@ -922,7 +922,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
 // (8 or 16 bytes).
 constexpr int kT128 = 128;
 
-template <class Op, MmaOut OUT, int NS>
+template <class Op, MmaOut OUT, int NS, bool STREAM = true>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch_p) {
   static_assert(NS == 2 || NS == 4, "stages in the ring: 4 (one workgroup per CU) or 2 (two)");
   constexpr uint32_t kStage = kT128 * kChunks * 16;       // 16 KB per operand and stage
@@ -1082,7 +1082,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
       if (gj >= p.n || i0 >= p.m) continue;
       const E v[4] = {(E)acc[i][j][0], (E)acc[i][j][1], (E)acc[i][j][2], (E)acc[i][j][3]};
       if constexpr (Epi<OUT>::kRun == 4) {
-        store_run<OUT>(p, i0, gj, v, 4, true);
+        store_run<OUT, STREAM>(p, i0, gj, v, 4, true);
       } else if (i0 + 4 <= p.m) {
         // 16-bit C: the run's 8 bytes, each value as Epi<OUT>::put_run
         // (or put_run_scaled) rounds it.
@@ -1104,7 +1104,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
         }
         *(u32x2*)c = o;
       } else {
-        store_run<OUT>(p, i0, gj, v, 4, false);
+        store_run<OUT, STREAM>(p, i0, gj, v, 4, false);
       }
     }
   cycle_record(p.probe, t0, probe_slot(wave), wave);
@@ -1380,6 +1380,8 @@ struct Plan {
 
 inline size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+inline bool split128_enabled() { return true; }
+
 template <class Op, MmaOut OUT>
 Plan make_plan(const GemmDesc& d) {
   constexpr int EB = Op::kElemBytes;
@@ -1471,6 +1473,22 @@ Plan make_plan(const GemmDesc& d) {
     return t;
   }
   if (d.batch != 1) return t;                       // split K: one problem only
+  // Long K on at most 128 tiles of 128x128: slices of at least 16 stages on
+  // them, at most 256 workgroups in all, partials summed by reduce_splits.
+  if (!kF32 && 2 * tiles128 <= kTn128MaxTiles && stages >= 32 && split128_enabled()) {
+    const int64_t sl = std::min<int64_t>({kTn128MaxTiles / tiles128, stages / 16, (int64_t)kMaxSplit});
+    const int64_t per = (stages + sl - 1) / sl;
+    const int64_t slices = (stages + per - 1) / per;
+    const int kslice = (int)per * (kFastKBytes / EB);
+    t.tn128 = true;
+    t.tn128_stages = 4;
+    t.split = (int)slices;
+    t.kslice = kslice;
+    t.k_last = d.k - (t.split - 1) * kslice;
+    t.ldw = ((int64_t)d.m + 7) / 8 * 8;
+    t.w_bytes = round256((size_t)t.split * t.ldw * d.n * 4);
+    return t;
+  }
   if ((!kF32 && tiles >= kSplitTiles) || stages < 16) return t;
   const int64_t min_per = tiles >= kSplitTiles ? 32 : 8;
   const int64_t mn = ((int64_t)d.m + 7) / 8 * 8 * d.n;
@@ -1595,10 +1613,20 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     q.alpha = 1.0f; q.beta = 0.0f; q.ialpha = 1; q.ibeta = 0;
     q.scale = nullptr;
     q.probe = nullptr;
-    q.tiles_m = (g->m + kFastTile - 1) / kFastTile;
-    q.tiles_n = (g->n + kFastTile - 1) / kFastTile;
-    hipLaunchKernelGGL((gemm_tn_fast<Op, RAW, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256), 0,
-                       s, q);
+    if constexpr (Op::kM16) {
+      if (t.tn128) {                  // slices on 128x128 tiles
+        q.tiles_m = (g->m + kT128 - 1) / kT128;
+        q.tiles_n = (g->n + kT128 - 1) / kT128;
+        hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256),
+                           0, s, q);
+      }
+    }
+    if (!t.tn128) {
+      q.tiles_m = (g->m + kFastTile - 1) / kFastTile;
+      q.tiles_n = (g->n + kFastTile - 1) / kFastTile;
+      hipLaunchKernelGGL((gemm_tn_fast<Op, RAW, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256), 0,
+                         s, q);
+    }
     constexpr int R = Epi<OUT>::kRun;
     const int64_t items = (int64_t)((g->m + R - 1) / R) * g->n;
     hipLaunchKernelGGL((reduce_splits<OUT, E>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,

@@ -66,7 +66,8 @@ def gemm_ex_case(blas, out_t, ta, tb, m, n, k, ldc_pad, seed, noalloc=False):
     ("tn256 one pass", BF16, 1, 0, 2944, 2944, 64, 8, "tn256", 0),
     ("tn256 one pass f32 C", F32, 1, 0, 2952, 2944, 80, 4, "tn256", 0),
     ("tn128, two-stage ring", BF16, 1, 0, 2312, 2184, 136, 8, "tn128", 0),
-    ("tn256 split K", BF16, 1, 0, 512, 2048, 4096, 8, "tn256", 2),
+    ("tn128 split K", BF16, 1, 0, 512, 2048, 4096, 8, "tn128", 2),
+    ("tn256 split K", BF16, 1, 0, 2048, 1152, 6144, 8, "tn256", 2),
     ("tn128", BF16, 1, 0, 1032, 1100, 200, 8, "tn128", 0),
     ("general64", BF16, 0, 1, 37, 29, 45, 3, "general64", 0),
     ("operand copies (N,N)", BF16, 0, 0, 320, 264, 512, 8, "tn128", 0),

@@ -191,19 +191,21 @@ def test_workspace_grows_and_follows_stream_changes():
 
 
 @pytest.mark.parametrize("in_t,out_t", [(BF16, BF16), (BF16, F32), (F16, F16), (F16, F32)])
-@pytest.mark.parametrize("m,n,k,alpha,beta,pad,cpad", [
-    (1024, 1024, 8192, 1.0, 0.0, 0, 0),      # 16 tiles, 128 stages
-    (300, 520, 4160, 2.5, -1.5, 8, 4),       # ragged m/n, last slice shorter
-    (512, 2048, 4096, 1.0, 0.0, 0, 8),       # 16 tiles, 64 stages
+@pytest.mark.parametrize("m,n,k,alpha,beta,pad,cpad,kernel", [
+    (1024, 1024, 8192, 1.0, 0.0, 0, 0, "tn128"),     # 64 tiles of 128x128, 128 stages
+    (300, 520, 4160, 2.5, -1.5, 8, 4, "tn128"),      # ragged m/n, last slice shorter
+    (512, 2048, 4096, 1.0, 0.0, 0, 8, "tn128"),      # 64 tiles, 64 stages
+    (2048, 1152, 6144, 1.0, 0.0, 0, 0, "tn256"),     # 144 tiles of 128x128: 256x256 slices
 ])
-def test_split_k_exact(blas, capfd, in_t, out_t, m, n, k, alpha, beta, pad, cpad):
-    """Problems with few 256x256 tiles and a long K are split along K; the
+def test_split_k_exact(blas, capfd, in_t, out_t, m, n, k, alpha, beta, pad, cpad, kernel):
+    """Problems with few tiles and a long K are split along K, on 128x128
+    tiles where at most 128 of them cover C, else on 256x256 tiles; the
     partial sums of exact inputs are exact, so the result stays bit-exact."""
     res = []
     plans = logged_plans(capfd, lambda: res.append(
         float_case(blas, in_t, out_t, 1, 0, m, n, k, alpha, beta, pad, cpad)))
     assert res == [(0, 0)]
-    assert len(plans) == 1 and plans[0]["kernel"] == "tn256" and int(plans[0]["split"]) >= 2, plans
+    assert len(plans) == 1 and plans[0]["kernel"] == kernel and int(plans[0]["split"]) >= 2, plans
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
@@ -231,7 +233,7 @@ def test_split_k_plan_limits(blas, capfd):
         lambda: blas.gemm_ex(1, 0, 256, 256, 8192, 1.0, buf.p, BF16, 8192, buf.p, BF16, 8192,
                              0.0, out.p, F32, 256),                   # the same, unbatched
     ]
-    for want, call in zip(["1", "1", "1", "16"], calls):
+    for want, call in zip(["1", "1", "1", "8"], calls):
         plans = logged_plans(capfd, lambda: (call() == g.SUCCESS) or pytest.fail("call failed"))
         g.synchronize()
         assert [p["split"] for p in plans] == [want], plans

@@ -51,7 +51,8 @@ def plant_specials(A: np.ndarray, B: np.ndarray, in_t: int) -> tuple[np.ndarray,
 @pytest.mark.parametrize("name,ta,tb,m,n,k,kernel,split", [
     ("tn256", 1, 0, 2944, 2944, 64, "tn256", False),     # over 512 tiles of 128x128
     ("general64", 1, 0, 37, 29, 45, "general64", False),
-    ("split K", 1, 0, 512, 2048, 4096, "tn256", True),
+    ("split K", 1, 0, 512, 2048, 4096, "tn128", True),
+    ("split K, 256x256 tiles", 1, 0, 2048, 1152, 6144, "tn256", True),
     ("tn128", 1, 0, 1032, 1100, 200, "tn128", False),
     ("operand copy (N,N)", 0, 0, 320, 264, 512, "tn128", False),
 ])
