@@ -906,15 +906,17 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
 // TN path, 128x128 tiles
 // ---------------------------------------------------------------------------
 
-// For 16-bit and int8 TN problems with few 256x256 tiles and short K, where
-// neither one pass of gemm_tn_fast nor a split fills the GPU cheaply. One
-// workgroup per CU, 4 waves of 64x64 per 128x128 tile, each wave 4 x 4 tiles
-// of 16x16 MFMAs accumulated in place in AGPRs (gemm_tn_fast's assembly
-// MFMA, fragment chunk order and stage swizzle at half the rows). K streams
-// through a ring of four 128-byte LDS stages (128 KB): three stages are in
-// flight while one is read, so a load has three stages of MFMA time to
-// land, and one barrier per stage both publishes the next stage and frees
-// the one the DMA refills. Fragments are double-buffered one k-step ahead,
+// For 16-bit and int8 TN problems of up to 512 tiles of 128x128 (make_plan:
+// one pass, or slices of K), where gemm_tn_fast's 256x256 tiles would leave
+// CUs idle. 4 waves of 64x64 per 128x128 tile, each wave 4 x 4 tiles of
+// 16x16 MFMAs accumulated in place in AGPRs (gemm_tn_fast's assembly MFMA,
+// fragment chunk order and stage swizzle at half the rows). K streams
+// through a ring of NS 128-byte LDS stages: with NS = 4 (128 KB, one
+// workgroup per CU) three stages are in flight while one is read, so a load
+// has three stages of MFMA time to land; with NS = 2 (64 KB) two workgroups
+// share a CU and each SIMD's second wave hides the shorter cover. One
+// barrier per stage both publishes the next stage and frees the one the DMA
+// refills. Fragments are double-buffered one k-step ahead,
 // read between the MFMAs. The DMA is issued as inline assembly: through the
 // builtin, the compiler's wait-count pass cannot tell the stage reads from
 // the DMA still landing in the other stages and waits for all of it before
@@ -1058,8 +1060,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     const int st = kt & (NS - 1);
     // k-step 0 of stage kt; its k-step 1 fragments read alongside
     kstep(IntC<0>{}, (uint32_t)st * kStage, 1, false, 0, 0);
-    // Stage kt+1 landed (stages kt+2, kt+3 may still be in flight), and no
-    // wave reads stage kt any more: its slot takes stage kt+NS.
+    // Stage kt+1 landed (with four stages, kt+2 and kt+3 may still be in
+    // flight), and no wave reads stage kt any more: its slot takes stage
+    // kt+NS.
     if constexpr (NS == 4) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
