@@ -56,12 +56,19 @@ struct SParams {
 // of 4 workgroups per CU), an XOR-swizzled unpadded layout (4 %), 32-deep
 // stages (2 workgroups per CU, 5-9 %), 256x256 tiles (one wave per SIMD,
 // 4 %), the next stage's LDS stores moved to mid-stage (no change).)
+//
+// MT = 32 (problems of few 64x64 tiles, 512^3 among them): each wave one
+// 16x16 tile with v_mfma_f32_16x16x4_f32, K 32 deep per stage (so that the
+// staging keeps one 4-element group per thread and operand), rows 48 floats
+// apart: the four 16-lane groups of a fragment read sit at k = 4s .. 4s+3,
+// 48 words apart, on four disjoint runs of 16 banks.
 template <int MT, bool VEC, bool TA, bool TB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
 void sgemm_mfma(SParams p) {
+  constexpr int kK = MT == 32 ? 32 : grxk::kK;   // K per stage
   constexpr int WT = MT / 2;            // wave tile edge
-  constexpr int NF = WT / 32;           // 32x32 MFMA tiles per wave edge
-  constexpr int PITCH = MT + 4;        // 16-byte aligned rows; 4 workgroups fit a CU's LDS at MT=128
+  constexpr int NF = WT / 32;           // 32x32 MFMA tiles per wave edge (0 at MT = 32)
+  constexpr int PITCH = MT == 32 ? 48 : MT + 4;  // 16-byte aligned rows; 4 workgroups fit a CU's LDS at MT=128
   constexpr int PER = MT * kK / 256;    // elements per thread per operand per stage
   __shared__ float As[2][kK][PITCH];
   __shared__ float Bs[2][kK][PITCH];
@@ -129,89 +136,131 @@ void sgemm_mfma(SParams p) {
     }
   };
 
-  f32x16 acc[NF][NF];
-#pragma unroll
-  for (int fm = 0; fm < NF; ++fm)
-#pragma unroll
-    for (int fn = 0; fn < NF; ++fn)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-
-  load(0);
-  store(0);
-  __syncthreads();
-  int buf = 0;
-  for (int k0 = 0; k0 < p.k; k0 += kK) {
-    const bool more = k0 + kK < p.k;
-    if (more) load(k0 + kK);
-    // Fragments one k-step ahead: step s+1's LDS reads are issued before
-    // step s's MFMAs (the scheduling barriers keep that order), so each
-    // wait covers reads issued a whole step earlier.
-    float av[2][NF], bv[2][NF];
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      av[0][f] = As[buf][hh][WT * wm + 32 * f + l32];
-      bv[0][f] = Bs[buf][hh][WT * wn + 32 * f + l32];
-    }
-#pragma unroll
-    for (int s = 0; s < kK / 2; ++s) {
-      if (s + 1 < kK / 2) {
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
-          av[(s + 1) & 1][f] = As[buf][2 * s + 2 + hh][WT * wm + 32 * f + l32];
-          bv[(s + 1) & 1][f] = Bs[buf][2 * s + 2 + hh][WT * wn + 32 * f + l32];
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int fm = 0; fm < NF; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < NF; ++fn)
-          acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s & 1][fm], bv[s & 1][fn], acc[fm][fn],
-                                                             0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (more) store(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-  }
-
-  // C = alpha*acc + beta*C (col-major); lane holds column l32 of each MFMA
-  // tile and rows 8*(r/4) + 4*hh + r%4: runs of 4 rows, one 16-byte
-  // non-temporal store each where the run lies inside C and C's columns are
-  // 16-byte aligned, element by element otherwise (same arithmetic).
+  // C = alpha*acc + beta*C (col-major) for a lane's run of 4 rows i0.. of
+  // column gj: one 16-byte non-temporal store where the run lies inside C and
+  // C's columns are 16-byte aligned, element by element otherwise (same
+  // arithmetic).
   const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)C & 15) == 0;
+  auto run4 = [&](int i0, int gj, const float* v) __attribute__((always_inline)) {
+    float* cp = C + (int64_t)gj * p.ldc + i0;
+    if (vec && i0 + 4 <= p.m) {
+      f32x4 o;
 #pragma unroll
-  for (int fm = 0; fm < NF; ++fm)
+      for (int q = 0; q < 4; ++q) o[q] = __fmul_rn(p.alpha, v[q]);
+      if (p.beta != 0.0f) {
+        const f32x4 old = *(const f32x4*)cp;
 #pragma unroll
-    for (int fn = 0; fn < NF; ++fn) {
-      const int gj = col0 + WT * wn + 32 * fn + l32;
-      if (gj >= p.n) continue;
+        for (int q = 0; q < 4; ++q) o[q] = __fadd_rn(o[q], __fmul_rn(p.beta, old[q]));
+      }
+      __builtin_nontemporal_store(o, (f32x4*)cp);
+    } else {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int i0 = row0 + WT * wm + 32 * fm + 8 * g + 4 * hh;
-        if (i0 >= p.m) continue;
-        float* cp = C + (int64_t)gj * p.ldc + i0;
-        if (vec && i0 + 4 <= p.m) {
-          f32x4 o;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) o[q] = __fmul_rn(p.alpha, acc[fm][fn][4 * g + q]);
-          if (p.beta != 0.0f) {
-            const f32x4 old = *(const f32x4*)cp;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) o[q] = __fadd_rn(o[q], __fmul_rn(p.beta, old[q]));
-          }
-          __builtin_nontemporal_store(o, (f32x4*)cp);
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if (i0 + q >= p.m) break;
-            const float v = __fmul_rn(p.alpha, acc[fm][fn][4 * g + q]);
-            cp[q] = (p.beta == 0.0f) ? v : __fadd_rn(v, __fmul_rn(p.beta, cp[q]));
-          }
-        }
+      for (int q = 0; q < 4; ++q) {
+        if (i0 + q >= p.m) break;
+        const float x = __fmul_rn(p.alpha, v[q]);
+        cp[q] = (p.beta == 0.0f) ? x : __fadd_rn(x, __fmul_rn(p.beta, cp[q]));
       }
     }
+  };
+
+  if constexpr (MT == 32) {
+    // One 16x16 tile per wave: lane l reads op(A) row 16*wm + l%16 and op(B)
+    // column 16*wn + l%16 at k = 4s + l/16, and holds rows 4*(l/16) .. +3 of
+    // column l%16 of the result.
+    const int r16 = lane & 15, kq = lane >> 4;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    load(0);
+    store(0);
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 < p.k; k0 += kK) {
+      const bool more = k0 + kK < p.k;
+      if (more) load(k0 + kK);
+      float av[kK / 4], bv[kK / 4];
+#pragma unroll
+      for (int st = 0; st < kK / 4; ++st) {
+        av[st] = As[buf][4 * st + kq][16 * wm + r16];
+        bv[st] = Bs[buf][4 * st + kq][16 * wn + r16];
+      }
+#pragma unroll
+      for (int st = 0; st < kK / 4; ++st)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st], bv[st], acc, 0, 0, 0);
+      if (more) store(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
+    const int gj = col0 + 16 * wn + r16;
+    const int i0 = row0 + 16 * wm + 4 * kq;
+    if (gj < p.n && i0 < p.m) {
+      const float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+      run4(i0, gj, v);
+    }
+  } else {
+    f32x16 acc[NF][NF];
+#pragma unroll
+    for (int fm = 0; fm < NF; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < NF; ++fn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+    load(0);
+    store(0);
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 < p.k; k0 += kK) {
+      const bool more = k0 + kK < p.k;
+      if (more) load(k0 + kK);
+      // Fragments one k-step ahead: step s+1's LDS reads are issued before
+      // step s's MFMAs (the scheduling barriers keep that order), so each
+      // wait covers reads issued a whole step earlier.
+      float av[2][NF], bv[2][NF];
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        av[0][f] = As[buf][hh][WT * wm + 32 * f + l32];
+        bv[0][f] = Bs[buf][hh][WT * wn + 32 * f + l32];
+      }
+#pragma unroll
+      for (int s = 0; s < kK / 2; ++s) {
+        if (s + 1 < kK / 2) {
+#pragma unroll
+          for (int f = 0; f < NF; ++f) {
+            av[(s + 1) & 1][f] = As[buf][2 * s + 2 + hh][WT * wm + 32 * f + l32];
+            bv[(s + 1) & 1][f] = Bs[buf][2 * s + 2 + hh][WT * wn + 32 * f + l32];
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int fm = 0; fm < NF; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < NF; ++fn)
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s & 1][fm], bv[s & 1][fn], acc[fm][fn],
+                                                               0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (more) store(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
+
+    // A lane holds column l32 of each MFMA tile and rows 8*(r/4) + 4*hh +
+    // r%4: runs of 4 rows.
+#pragma unroll
+    for (int fm = 0; fm < NF; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < NF; ++fn) {
+        const int gj = col0 + WT * wn + 32 * fn + l32;
+        if (gj >= p.n) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int i0 = row0 + WT * wm + 32 * fm + 8 * g + 4 * hh;
+          if (i0 >= p.m) continue;
+          const float v[4] = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                              acc[fm][fn][4 * g + 3]};
+          run4(i0, gj, v);
+        }
+      }
+  }
   cycle_record(p.probe, t0, (uint32_t)((bz * gridDim.x + blockIdx.x) * 4 + wave), wave);
 }
 
@@ -294,9 +343,12 @@ hipError_t launch_sgemm(const SgemmDesc& d, hipStream_t s) {
   p.alpha = d.alpha; p.beta = d.beta;
   p.probe = d.probe;
   if (d.batch > 65535) return hipErrorInvalidValue;
-  // 128-wide tiles once they fill the chip, 64-wide below that.
+  // 128-wide tiles once they fill the chip, 64-wide below that, 32-wide
+  // where 64-wide tiles would leave half the CUs idle (without a cycle
+  // probe, whose slots are counted for 64x64 tiles).
   const int64_t big = ((int64_t)(d.m + 127) / 128) * ((d.n + 127) / 128) * d.batch;
-  const int mt = big >= 256 ? 128 : 64;
+  const int64_t mid = ((int64_t)(d.m + 63) / 64) * ((d.n + 63) / 64) * d.batch;
+  const int mt = big >= 256 ? 128 : (mid >= 128 || d.probe ? 64 : 32);
   p.tiles_m = (d.m + mt - 1) / mt;
   const int64_t tiles = (int64_t)p.tiles_m * ((d.n + mt - 1) / mt);
   if (tiles > 0x7fffffff) return hipErrorInvalidValue;
@@ -304,8 +356,16 @@ hipError_t launch_sgemm(const SgemmDesc& d, hipStream_t s) {
                    (uintptr_t)d.a % 16 == 0 && (uintptr_t)d.b % 16 == 0;
   const dim3 grid((unsigned)tiles, 1, (unsigned)d.batch);
   auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, p); };
-  const int sel = (mt == 128 ? 8 : 0) | (vec ? 4 : 0) | (d.ta ? 2 : 0) | (d.tb ? 1 : 0);
+  const int sel = (mt == 128 ? 8 : mt == 32 ? 16 : 0) | (vec ? 4 : 0) | (d.ta ? 2 : 0) | (d.tb ? 1 : 0);
   switch (sel) {
+    case 16: go(sgemm_mfma<32, false, false, false>); break;
+    case 17: go(sgemm_mfma<32, false, false, true>); break;
+    case 18: go(sgemm_mfma<32, false, true, false>); break;
+    case 19: go(sgemm_mfma<32, false, true, true>); break;
+    case 20: go(sgemm_mfma<32, true, false, false>); break;
+    case 21: go(sgemm_mfma<32, true, false, true>); break;
+    case 22: go(sgemm_mfma<32, true, true, false>); break;
+    case 23: go(sgemm_mfma<32, true, true, true>); break;
     case 0:  go(sgemm_mfma<64, false, false, false>); break;
     case 1:  go(sgemm_mfma<64, false, false, true>); break;
     case 2:  go(sgemm_mfma<64, false, true, false>); break;
@@ -321,7 +381,8 @@ hipError_t launch_sgemm(const SgemmDesc& d, hipStream_t s) {
     case 12: go(sgemm_mfma<128, true, false, false>); break;
     case 13: go(sgemm_mfma<128, true, false, true>); break;
     case 14: go(sgemm_mfma<128, true, true, false>); break;
-    default: go(sgemm_mfma<128, true, true, true>); break;
+    case 15: go(sgemm_mfma<128, true, true, true>); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
