@@ -53,10 +53,12 @@ def test_reference_cycle_benchmark_runs_on_mi355x(gpu):
     more than a fifth of sgemm's cycles per element, ref
     tests/bench/gemm_cycles.cpp:238-299) and its two k-sweep checks state the
     reference's simulator model; on gfx950 both calls are one workgroup of
-    fixed cost at these shapes, and all three fail (GemmEx 0.4-0.55x of
-    Sgemm per element; profiles/reference_gemm_cycles_gate.md). Asserted:
-    the two measurement checks that hold, and that those three are the only
-    failures."""
+    fixed cost at these shapes, so the gate fails (GemmEx 0.4-0.55x of
+    Sgemm per element; profiles/reference_gemm_cycles_gate.md), and so,
+    almost always, do the two k-sweep checks, whose spans are then mostly
+    that fixed cost: timing noise has passed one of them now and then.
+    Asserted: the two measurement checks that hold, the gate's failure, and
+    that no check outside those three fails."""
     r = _run("gemm_cycles")
     assert r.returncode == 1, (r.returncode, r.stdout[-3000:], r.stderr[-2000:])
     out = r.stdout
@@ -64,9 +66,8 @@ def test_reference_cycle_benchmark_runs_on_mi355x(gpu):
     assert "ok    the tensor path was measured at every shape" in out
     fails = sorted(line.strip()[len("FAIL"):].strip() for line in out.splitlines()
                    if line.strip().startswith("FAIL  "))
-    assert fails == sorted([
-        "GemmEx costs at most a fifth of sgemm per output element",
-        "cost per element grows with k",
-        "cost per multiply-add is roughly constant, as an unblocked loop should be",
-    ]), fails
-    assert "FAILED (3)" in out
+    gate = "GemmEx costs at most a fifth of sgemm per output element"
+    k_sweep = {"cost per element grows with k",
+               "cost per multiply-add is roughly constant, as an unblocked loop should be"}
+    assert gate in fails and set(fails) <= k_sweep | {gate}, fails
+    assert f"FAILED ({len(fails)})" in out
