@@ -241,7 +241,13 @@ grxblasStatus_t launch_gemm(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut ou
 // until the launch is recorded, so calls on other streams wait for it.
 grxblasStatus_t launch_gemm_noalloc(grxblasContext& ctx, grxk::MmaIn in, grxk::MmaOut out,
                                     grxk::GemmDesc& d) {
-  const size_t need = grxk::gemm_workspace_bytes(in, out, d);
+  size_t need = grxk::gemm_workspace_bytes(in, out, d);
+  if (need > grxk::kNoAllocScratchBytes) {
+    // Padded copies of both operands (K not a multiple of 16 bytes) that do
+    // not fit the scratch: the plan without them (the general path).
+    d.pad_copies = false;
+    need = grxk::gemm_workspace_bytes(in, out, d);
+  }
   if (need > grxk::kNoAllocScratchBytes) {
     std::fprintf(stderr,
                  "grxblas: grxblasGemmExNoAlloc: this problem needs %zu bytes of scratch "

@@ -1200,14 +1200,16 @@ __global__ __launch_bounds__(256) void gemm_general(KParams batch_p) {
 // operand transpose (for layouts the TN kernel cannot read directly)
 // ---------------------------------------------------------------------------
 
-// Y[c + r*ldy] = X[r + c*ldx] for r < R, c < C, elements of EB bytes; batch
-// blockIdx.z at X + z*sx, Y + z*sy (elements). 64x64-element tiles through
-// LDS: 16-byte loads along r, 16-byte stores along c. C is a multiple of
-// 16/EB (the caller's k), so an output chunk is wholly inside or outside.
+// Y[c + r*ldy] = X[r + c*ldx] for r < R, c < C, elements of EB bytes, with
+// X read only for c < Cin (columns Cin .. C-1 of Y are zeros: K padded to a
+// multiple of 16 bytes); batch blockIdx.z at X + z*sx, Y + z*sy (elements).
+// 64x64-element tiles through LDS: 16-byte loads along r, 16-byte stores
+// along c. C is a multiple of 16/EB, so an output chunk is wholly inside or
+// outside.
 template <int EB>
 __global__ __launch_bounds__(256) void transpose_k(const uint8_t* X, int64_t ldx, int64_t sx,
                                                    uint8_t* Y, int64_t ldy, int64_t sy, int R,
-                                                   int C, int vec_in) {
+                                                   int C, int Cin, int vec_in) {
   constexpr int T = 64;
   constexpr int VE = 16 / EB;        // elements per 16-byte chunk
   constexpr int CPS = T / VE;        // chunks per 64-element segment
@@ -1221,13 +1223,13 @@ __global__ __launch_bounds__(256) void transpose_k(const uint8_t* X, int64_t ldx
     const int gc = c0 + c, gr = r0 + ch * VE;
     uint8_t* dst = &tile[c][ch * 16];
     const uint8_t* src = X + ((int64_t)gc * ldx + gr) * EB;
-    if (vec_in && gc < C && gr + VE <= R) {
+    if (vec_in && gc < Cin && gr + VE <= R) {
       *(u32x4*)dst = *(const u32x4*)src;
     } else {
 #pragma unroll
       for (int e = 0; e < VE; ++e)
 #pragma unroll
-        for (int b = 0; b < EB; ++b) dst[e * EB + b] = (gc < C && gr + e < R) ? src[e * EB + b] : 0;
+        for (int b = 0; b < EB; ++b) dst[e * EB + b] = (gc < Cin && gr + e < R) ? src[e * EB + b] : 0;
     }
   }
   __syncthreads();
@@ -1257,11 +1259,63 @@ __global__ __launch_bounds__(256) void transpose_k(const uint8_t* X, int64_t ldx
 
 template <int EB>
 hipError_t launch_transpose(const void* x, int64_t ldx, int64_t sx, void* y, int64_t ldy,
-                            int64_t sy, int R, int C, int batch, hipStream_t s) {
+                            int64_t sy, int R, int C, int Cin, int batch, hipStream_t s) {
   const int vec_in = ((uintptr_t)x % 16 == 0) && (ldx * EB) % 16 == 0 && (sx * EB) % 16 == 0;
   const dim3 grid((unsigned)((R + 63) / 64), (unsigned)((C + 63) / 64), (unsigned)batch);
   hipLaunchKernelGGL((transpose_k<EB>), grid, dim3(256), 0, s, (const uint8_t*)x, ldx, sx,
-                     (uint8_t*)y, ldy, sy, R, C, vec_in);
+                     (uint8_t*)y, ldy, sy, R, C, Cin, vec_in);
+  return hipGetLastError();
+}
+
+// Y[c + r*ldy] = X[c + r*ldx] for r < R, c < Cin, zeros for Cin <= c < C
+// (C a multiple of 16/EB): an operand that is already K-contiguous but whose
+// K, leading dimension or base the TN kernels cannot take, re-laid in rows of
+// C elements (K padded to 16 bytes). One 16-byte output chunk per thread; a
+// chunk wholly inside the row reads the aligned dwords that hold its 16
+// bytes (four, or five when the source is not 4-byte aligned) and shifts
+// them into place with v_alignbyte; every dword read holds at least one of
+// the chunk's own bytes, so none can fall outside the source's mapped pages.
+// The row's last, partial chunk is read element by element. Batch
+// blockIdx.y at X + z*sx, Y + z*sy (elements).
+template <int EB>
+__global__ __launch_bounds__(256) void repitch_k(const uint8_t* X, int64_t ldx, int64_t sx,
+                                                 uint8_t* Y, int64_t ldy, int64_t sy, int R,
+                                                 int C, int Cin) {
+  constexpr int VE = 16 / EB;
+  const int cpr = C / VE;                                  // chunks per row
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= (int64_t)R * cpr) return;
+  const int r = (int)(q / cpr), c0 = (int)(q % cpr) * VE;
+  const uint8_t* src = X + ((int64_t)blockIdx.y * sx + (int64_t)r * ldx + c0) * EB;
+  u32x4 o;
+  if (c0 + VE <= Cin) {
+    const uintptr_t a = (uintptr_t)src;
+    const uint32_t sh = (uint32_t)(a & 3);
+    const uint32_t* w = (const uint32_t*)(a - sh);
+    uint32_t d[5];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[i] = w[i];
+    d[4] = sh ? w[4] : 0u;                   // the dword holding byte a+15 when unaligned
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
+  } else {
+    uint8_t w[16];
+#pragma unroll
+    for (int e = 0; e < VE; ++e)
+#pragma unroll
+      for (int b = 0; b < EB; ++b) w[e * EB + b] = c0 + e < Cin ? src[e * EB + b] : 0;
+    o = *(const u32x4*)w;
+  }
+  *(u32x4*)(Y + ((int64_t)blockIdx.y * sy + (int64_t)r * ldy + c0) * EB) = o;
+}
+
+template <int EB>
+hipError_t launch_repitch(const void* x, int64_t ldx, int64_t sx, void* y, int64_t ldy, int64_t sy,
+                          int R, int C, int Cin, int batch, hipStream_t s) {
+  const int64_t chunks = (int64_t)R * (C / (16 / EB));
+  const dim3 grid((unsigned)((chunks + 255) / 256), (unsigned)batch);
+  hipLaunchKernelGGL((repitch_k<EB>), grid, dim3(256), 0, s, (const uint8_t*)x, ldx, sx,
+                     (uint8_t*)y, ldy, sy, R, C, Cin);
   return hipGetLastError();
 }
 
@@ -1367,6 +1421,7 @@ constexpr int64_t kStageNsF32 = 7070;
 
 struct Plan {
   bool copy_a = false, copy_b = false;
+  int kp = 0;                     // the copies' K (row length): K, or K padded to 16 bytes
   int batch_a = 0, batch_b = 0;   // copies made (1 when the stride broadcasts)
   size_t a_bytes = 0, b_bytes = 0;
   int split = 1;                  // K slices
@@ -1417,6 +1472,41 @@ Plan make_plan(const GemmDesc& d) {
     GemmDesc q = c.e;
     if (c.copy_a) q.a = (const void*)(uintptr_t)256;
     if (c.copy_b) q.b = (const void*)(uintptr_t)256;
+    if (tn_ready<Op, OUT>(q)) {
+      c.tn = true;
+      c.kp = d.k;
+      t = c;
+    }
+  }
+  // (16-bit and int8 inputs; fp32 keeps sgemm_mfma, whose guarded staging
+  // takes any K at its usual rate.)
+  if (!std::is_same<Op, OpF32>::value && !t.tn && d.pad_copies && d.k > 0 &&
+      (int64_t)d.m * d.n * d.k >= kTransposeMinWork) {
+    // K not a multiple of 16 bytes, or the K-contiguous operand unaligned:
+    // both operands copied K-contiguous into rows of K rounded up to 16
+    // bytes, the pad zero in both (so every padded product is an exact
+    // zero), then the TN kernels on K' (4096^2 x 4095 bf16: 47 TFLOP/s on
+    // the 64x64 general kernel). An operand stored K-contiguous is re-laid
+    // row by row (repitch_k), the other transposed (transpose_k).
+    constexpr int VE = 16 / EB;
+    const int kp = (d.k + VE - 1) / VE * VE;
+    Plan c = t;
+    c.copy_a = c.copy_b = true;
+    c.kp = kp;
+    c.batch_a = d.stride_a == 0 ? 1 : d.batch;
+    c.a_bytes = round256((size_t)c.batch_a * d.m * kp * EB);
+    c.batch_b = d.stride_b == 0 ? 1 : d.batch;
+    c.b_bytes = round256((size_t)c.batch_b * d.n * kp * EB);
+    c.e.ta = true;
+    c.e.tb = false;
+    c.e.k = kp;
+    c.e.lda = kp;
+    c.e.ldb = kp;
+    c.e.stride_a = d.stride_a == 0 ? 0 : (int64_t)d.m * kp;
+    c.e.stride_b = d.stride_b == 0 ? 0 : (int64_t)d.n * kp;
+    GemmDesc q = c.e;
+    q.a = (const void*)(uintptr_t)256;
+    q.b = (const void*)(uintptr_t)256;
     if (tn_ready<Op, OUT>(q)) {
       c.tn = true;
       t = c;
@@ -1487,7 +1577,7 @@ Plan make_plan(const GemmDesc& d) {
     t.tn128_stages = 4;
     t.split = (int)slices;
     t.kslice = kslice;
-    t.k_last = d.k - (t.split - 1) * kslice;
+    t.k_last = t.e.k - (t.split - 1) * kslice;
     t.ldw = ((int64_t)d.m + 7) / 8 * 8;
     t.w_bytes = round256((size_t)t.split * t.ldw * d.n * 4);
     return t;
@@ -1520,7 +1610,7 @@ Plan make_plan(const GemmDesc& d) {
   t.split = split;
   t.split_ns = best;
   t.kslice = kslice;
-  t.k_last = d.k - (split - 1) * kslice;
+  t.k_last = t.e.k - (split - 1) * kslice;
   t.ldw = ((int64_t)d.m + 7) / 8 * 8;
   t.w_bytes = round256((size_t)split * t.ldw * d.n * 4);
   return t;
@@ -1563,16 +1653,24 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   }
   uint8_t* ws = (uint8_t*)d.ws;
   if (t.copy_a) {
-    // A (m x k, m contiguous) -> A^T rows of k
-    const hipError_t e = launch_transpose<EB>(d.a, d.lda, d.stride_a, ws, d.k,
-                                              (int64_t)d.m * d.k, d.m, d.k, t.batch_a, s);
+    // op(A) as rows of kp: A (m x k, m contiguous) transposed, or A^T (rows
+    // of k) re-laid; columns k .. kp-1 zero
+    const hipError_t e =
+        d.ta ? launch_repitch<EB>(d.a, d.lda, d.stride_a, ws, t.kp, (int64_t)d.m * t.kp, d.m, t.kp,
+                                  d.k, t.batch_a, s)
+             : launch_transpose<EB>(d.a, d.lda, d.stride_a, ws, t.kp, (int64_t)d.m * t.kp, d.m,
+                                    t.kp, d.k, t.batch_a, s);
     if (e != hipSuccess) return e;
     t.e.a = ws;
   }
   if (t.copy_b) {
-    // B (n x k, n contiguous) -> rows of k per column j
-    const hipError_t e = launch_transpose<EB>(d.b, d.ldb, d.stride_b, ws + t.a_bytes, d.k,
-                                              (int64_t)d.n * d.k, d.n, d.k, t.batch_b, s);
+    // op(B) as rows of kp per column j: B (k x n, k contiguous) re-laid, or
+    // B^T (n contiguous) transposed
+    const hipError_t e =
+        !d.tb ? launch_repitch<EB>(d.b, d.ldb, d.stride_b, ws + t.a_bytes, t.kp, (int64_t)d.n * t.kp,
+                                   d.n, t.kp, d.k, t.batch_b, s)
+              : launch_transpose<EB>(d.b, d.ldb, d.stride_b, ws + t.a_bytes, t.kp,
+                                     (int64_t)d.n * t.kp, d.n, t.kp, d.k, t.batch_b, s);
     if (e != hipSuccess) return e;
     t.e.b = ws + t.a_bytes;
   }

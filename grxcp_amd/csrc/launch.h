@@ -35,6 +35,10 @@ struct GemmDesc {
   int64_t stride_a = 0, stride_b = 0, stride_c = 0;  // elements, signed
   void* ws = nullptr;       // device workspace for transposed operand copies
   size_t ws_bytes = 0;
+  // K not a multiple of 16 bytes (or an operand the TN kernels cannot read
+  // as it lies) may be served by copies of both operands with K padded with
+  // zeros; false keeps such a problem on the general path (no workspace).
+  bool pad_copies = true;
 };
 
 // Picks the kernel (TN fast path, TN fast path behind transposed copies of

@@ -330,6 +330,40 @@ def test_tn128_two_stage_ring_exact(blas, capfd):
     assert not bad, bad
 
 
+@pytest.mark.parametrize("kind,ta,tb,it,ot,k,pad", [
+    ("f", 1, 0, BF16, BF16, 1001, 0),   # T,N, K not a multiple of 8
+    ("f", 0, 0, F16, F32, 1003, 0),     # N,N
+    ("f", 1, 1, BF16, F32, 997, 0),     # T,T
+    ("f", 0, 1, F16, F16, 999, 0),      # N,T
+    ("f", 1, 0, BF16, BF16, 1024, 1),   # K aligned, lda / ldb odd
+    ("i8", 1, 0, None, None, 1001, 0),  # int8: K not a multiple of 16
+    ("dq", 0, 0, None, None, 1007, 0),
+])
+def test_padded_copies_for_unaligned_k(blas, capfd, kind, ta, tb, it, ot, k, pad):
+    """K not a multiple of 16 bytes, or operands the TN kernels cannot read as
+    they lie, above the copy threshold: both operands are copied K-contiguous
+    into rows of K padded with zeros, then the TN kernels run on the padded
+    K. Bit-exact over the padded C with guard bands, and the plan shows both
+    copies on a TN kernel (no general path)."""
+    m, n = 1032, 1100
+    res = []
+    if kind == "f":
+        call = lambda: res.append(float_case(blas, it, ot, ta, tb, m, n, k, 1.5, -0.5, pad, 0,  # noqa: E731
+                                             seed=k + pad, guard=True))
+        ok = (0, 0)
+    elif kind == "i8":
+        call = lambda: res.append(int8_case(blas, ta, tb, m, n, k, 2.0, 1.0, pad, fill="rand",  # noqa: E731
+                                            seed=k, cpad=0, guard=True))
+        ok = 0
+    else:
+        call = lambda: res.append(dequant_case(blas, ta, tb, m, n, k, pad, 0, seed=k, guard=True))  # noqa: E731
+        ok = (0, 0)
+    plans = logged_plans(capfd, call)
+    assert res == [ok], res
+    assert len(plans) == 1 and plans[0]["kernel"] in ("tn128", "tn256"), plans
+    assert plans[0]["copy_a"] == "1" and plans[0]["copy_b"] == "1", plans
+
+
 def test_split_k_workspaces_on_many_streams():
     """Split-K calls rotating over six streams (more than the handle keeps
     workspaces for per device, so workspaces are handed over) with no host

@@ -101,6 +101,31 @@ def test_noalloc_refuses_more_scratch_than_it_holds(blas, capfd):
     assert np.array_equal(dC.download(np.uint32, m * n), poison)
 
 
+def test_noalloc_without_room_for_padded_copies_takes_the_general_path(blas, capfd):
+    """K not a multiple of 16 bytes: grxblasGemmEx pads it in copies of both
+    operands. Where those copies exceed the 64 MiB scratch (2048 x 2048 x
+    8199 bf16: 67 MB) the allocation-free entry point runs the plan without
+    them, the general kernel, rather than refusing a problem it ran before
+    such copies existed. Exact inputs (halves), so both give the same bits."""
+    import oracle as O
+    m, n, k = 2048, 2048, 8199
+    st = O.HalvesStream(77)
+    dA, dB = to_dev(O.f32_to_bf16(st.take(m * k))), to_dev(O.f32_to_bf16(st.take(k * n)))
+    got, plans = [], []
+    for fn in (blas.gemm_ex, blas.gemm_ex_noalloc):
+        dC = g.DeviceBuffer(m * n * 4)
+        say(f"padded-copy plan {m}x{n}x{k} through {fn.__name__}")
+        status = []
+        plans += logged_plans(capfd, lambda: status.append(  # noqa: B023
+            fn(1, 0, m, n, k, 1.0, dA.p, BF16, k, dB.p, BF16, k, 0.0, dC.p, F32, m)))
+        g.synchronize()
+        assert status == [g.SUCCESS], status
+        got.append(dC.download(np.float32, m * n))
+    assert [(p["kernel"], p["copy_a"], p["copy_b"]) for p in plans] == \
+        [("tn128", "1", "1"), ("general64", "0", "0")], plans
+    assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))
+
+
 def _bf16_operands(r, m, n, k):
     A = synth.f32_to_bf16_bits(r.standard_normal(m * k).astype(np.float32))
     B = synth.f32_to_bf16_bits(r.standard_normal(n * k).astype(np.float32))
