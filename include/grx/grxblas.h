@@ -178,10 +178,10 @@ grxblasStatus_t grxblasSetTensorMapSlots(grxblasHandle_t handle,
                                          int slotA, int slotB);
 
 /* The matrix-core tile one wavefront computes per instruction on GemmEx's
- * general path, which unaligned problems and small ones in layouts other
+ * general path, which small problems that are unaligned or in layouts other
  * than (T,N) take (ref grxblas.h:142-143): 32 x 32 x 16 for fp16/bf16
  * (v_mfma_f32_32x32x16_*; int8 32 x 32 x 32). Aligned (T,N) problems, and
- * larger ones of other layouts behind an operand copy, run 16 x 16 x 32
+ * larger ones behind operand copies, run 16 x 16 x 32
  * instructions (int8 16 x 16 x 64): eight by eight per wavefront on 256 x
  * 256 tiles, four by four on 128 x 128 tiles. */
 grxblasStatus_t grxblasGetTensorTile(grxblasHandle_t handle,
