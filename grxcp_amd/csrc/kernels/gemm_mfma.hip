@@ -1372,7 +1372,9 @@ __global__ __launch_bounds__(256) void reduce_splits(KParams p, const E* ws, int
     for (int h = 0; h < H; ++h) w[h] = *(const i32x4*)(src + z * sstride + 4 * h);
     add(w);
   }
-  store_run<OUT>(p, i0, j, v, R, true);
+  // Runs of C are 16-byte aligned unless C is staged (ldc or base off 16 bytes).
+  using T = typename Epi<OUT>::T;
+  store_run<OUT>(p, i0, j, v, R, ((uintptr_t)((T*)p.c + (int64_t)j * p.ldc + i0) & 15) == 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1422,6 +1424,7 @@ constexpr int64_t kStageNsF32 = 7070;
 struct Plan {
   bool copy_a = false, copy_b = false;
   int kp = 0;                     // the copies' K (row length): K, or K padded to 16 bytes
+  bool c_staged = false;          // C reached through raw partials and reduce_splits
   int batch_a = 0, batch_b = 0;   // copies made (1 when the stride broadcasts)
   size_t a_bytes = 0, b_bytes = 0;
   int split = 1;                  // K slices
@@ -1441,7 +1444,7 @@ inline size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
 inline bool split128_enabled() { return true; }
 
 template <class Op, MmaOut OUT>
-Plan make_plan(const GemmDesc& d) {
+Plan make_plan_core(const GemmDesc& d) {
   constexpr int EB = Op::kElemBytes;
   Plan t;
   t.e = d;
@@ -1616,6 +1619,44 @@ Plan make_plan(const GemmDesc& d) {
   return t;
 }
 
+// C whose leading dimension, base or batch stride is not on 16 bytes, which
+// the TN kernels' stores need (bf16 C with m = 4095, or ldc = 500): 16-bit
+// and int8 problems of one batch above the copy threshold keep the TN plan
+// they would have with C aligned, their K loop writing raw partials (one
+// slice, or the plan's split) to the workspace, and reduce_splits applies
+// alpha, beta and the conversion into C, run by run.
+template <MmaOut OUT>
+bool c_ready(const GemmDesc& d) {
+  constexpr int OB = out_bytes<OUT>();
+  return (d.ldc * OB) % 16 == 0 && ((uintptr_t)d.c % 16) == 0 && (d.stride_c * OB) % 16 == 0;
+}
+
+template <class Op, MmaOut OUT>
+Plan make_plan(const GemmDesc& d) {
+  Plan t = make_plan_core<Op, OUT>(d);
+  if (t.tn || std::is_same<Op, OpF32>::value || d.batch != 1 || d.probe || !d.pad_copies ||
+      d.k <= 0 || (int64_t)d.m * d.n * d.k < kTransposeMinWork || c_ready<OUT>(d))
+    return t;
+  GemmDesc q = d;
+  q.c = (void*)(uintptr_t)256;
+  q.ldc = ((int64_t)d.m + 7) / 8 * 8;
+  q.stride_c = 0;
+  Plan c = make_plan_core<Op, OUT>(q);
+  if (!c.tn) return t;
+  c.e.c = d.c;
+  c.e.ldc = d.ldc;
+  c.e.stride_c = d.stride_c;
+  c.c_staged = true;
+  if (c.split <= 1) {
+    c.split = 1;
+    c.kslice = c.e.k;
+    c.k_last = c.e.k;
+    c.ldw = ((int64_t)d.m + 7) / 8 * 8;
+    c.w_bytes = round256((size_t)c.ldw * d.n * 4);
+  }
+  return c;
+}
+
 // GRXBLAS_LOG set (and not "0"): one line on stderr per GemmEx-family call
 // naming the path it took. Read on every call, so it can be switched at run time.
 inline bool log_plans() {
@@ -1678,10 +1719,10 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   if (log_plans()) {
     std::fprintf(stderr,
                  "grxblas: gemm %s->%s ta=%d tb=%d m=%d n=%d k=%d batch=%d kernel=%s copy_a=%d "
-                 "copy_b=%d split=%d ring=%d\n",
+                 "copy_b=%d split=%d ring=%d staged=%d\n",
                  Op::kName, out_name<OUT>(), (int)d.ta, (int)d.tb, d.m, d.n, d.k, d.batch,
                  t.tn ? (t.tn128 ? "tn128" : "tn256") : "general64", (int)t.copy_a, (int)t.copy_b, t.split,
-                 t.tn && t.tn128 ? t.tn128_stages : 0);
+                 t.tn && t.tn128 ? t.tn128_stages : 0, (int)(t.tn && t.c_staged));
   }
 
   KParams p{};
@@ -1700,8 +1741,9 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   p.sb = g->stride_b * EB;
   p.sc = g->stride_c * out_bytes<OUT>();
 
-  if (t.tn && t.split > 1) {
-    // Slices: raw partials into the workspace, then the epilogue over their sum.
+  if (t.tn && (t.split > 1 || t.c_staged)) {
+    // Slices (or one, for a staged C): raw partials into the workspace, then
+    // the epilogue over their sum.
     KParams q = p;
     E* w = (E*)(ws + t.a_bytes + t.b_bytes);
     q.c = w;
@@ -1718,8 +1760,12 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
       if (t.tn128) {                  // slices on 128x128 tiles
         q.tiles_m = (g->m + kT128 - 1) / kT128;
         q.tiles_n = (g->n + kT128 - 1) / kT128;
-        hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256),
-                           0, s, q);
+        if (t.tn128_stages == 2)
+          hipLaunchKernelGGL((gemm_tn128<Op, RAW, 2, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256),
+                             0, s, q);
+        else
+          hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256),
+                             0, s, q);
       }
     }
     if (!t.tn128) {

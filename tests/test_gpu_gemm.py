@@ -364,6 +364,39 @@ def test_padded_copies_for_unaligned_k(blas, capfd, kind, ta, tb, it, ot, k, pad
     assert plans[0]["copy_a"] == "1" and plans[0]["copy_b"] == "1", plans
 
 
+@pytest.mark.parametrize("kind,ta,tb,it,ot,m,k", [
+    ("f", 1, 0, BF16, BF16, 1031, 1024),   # bf16 C, ldc = 1031
+    ("f", 1, 0, F16, F32, 1030, 1000),     # fp32 C, ldc * 4 = 4120
+    ("f", 0, 0, BF16, BF16, 1027, 1001),   # (N, N), K and C unaligned: padded copies, staged C
+    ("f", 1, 0, BF16, F32, 1030, 8192),    # long K: slices, then the staged C
+    ("i8", 1, 0, None, None, 1030, 1024),  # int32 C
+    ("dq", 1, 0, None, None, 1027, 1024),  # dequantised bf16 C
+])
+def test_staged_c_for_unaligned_ldc(blas, capfd, kind, ta, tb, it, ot, m, k):
+    """C whose columns are not on 16-byte boundaries (ldc = m, m not a
+    multiple of 8 for 16-bit C, of 4 for 32-bit C) above the copy threshold:
+    the TN kernels write raw partials to the workspace and reduce_splits
+    applies alpha, beta and the conversion into C. Bit-exact over the padded
+    C with guard bands; the plan shows a TN kernel with C staged."""
+    n = 1100
+    res = []
+    if kind == "f":
+        call = lambda: res.append(float_case(blas, it, ot, ta, tb, m, n, k, 1.5, -0.5, 0, 0,  # noqa: E731
+                                             seed=m + k, guard=True))
+        ok = (0, 0)
+    elif kind == "i8":
+        call = lambda: res.append(int8_case(blas, ta, tb, m, n, k, 2.0, 1.0, 0, fill="rand",  # noqa: E731
+                                            seed=m, cpad=0, guard=True))
+        ok = 0
+    else:
+        call = lambda: res.append(dequant_case(blas, ta, tb, m, n, k, 0, 0, seed=m, guard=True))  # noqa: E731
+        ok = (0, 0)
+    plans = logged_plans(capfd, call)
+    assert res == [ok], res
+    assert len(plans) == 1 and plans[0]["kernel"] in ("tn128", "tn256"), plans
+    assert plans[0]["staged"] == "1", plans
+
+
 def test_split_k_workspaces_on_many_streams():
     """Split-K calls rotating over six streams (more than the handle keeps
     workspaces for per device, so workspaces are handed over) with no host
