@@ -243,8 +243,9 @@ grxblasStatus_t launch_gemm_noalloc(grxblasContext& ctx, grxk::MmaIn in, grxk::M
                                     grxk::GemmDesc& d) {
   size_t need = grxk::gemm_workspace_bytes(in, out, d);
   if (need > grxk::kNoAllocScratchBytes) {
-    // Padded copies of both operands (K not a multiple of 16 bytes) that do
-    // not fit the scratch: the plan without them (the general path).
+    // Padded copies of both operands (K not a multiple of 16 bytes) or a
+    // staged C that do not fit the scratch: the plan without them (the
+    // general path).
     d.pad_copies = false;
     need = grxk::gemm_workspace_bytes(in, out, d);
   }

@@ -37,7 +37,8 @@ struct GemmDesc {
   size_t ws_bytes = 0;
   // K not a multiple of 16 bytes (or an operand the TN kernels cannot read
   // as it lies) may be served by copies of both operands with K padded with
-  // zeros; false keeps such a problem on the general path (no workspace).
+  // zeros, and C off 16-byte boundaries through raw partials in the
+  // workspace; false keeps such a problem on the general path.
   bool pad_copies = true;
 };
 
