@@ -169,6 +169,24 @@ def test_batched_runs_the_128_tile_kernel(blas, capfd):
     assert not bad, bad
 
 
+def test_batched_padded_copies_for_unaligned_k(blas, capfd):
+    """K not a multiple of 16 bytes above the copy threshold, in a batch:
+    both operands are copied per batch (once where a stride of 0 broadcasts)
+    into rows of K padded with zeros, then the TN kernel; every batch
+    bit-exact, C gaps untouched, both copies in the plan."""
+    from test_gpu_gemm import logged_plans
+    cases = [(BF16, BF16, 256, 264, 1001, 2, "packed", "zero", "gap"),
+             (I8, I32, 256, 256, 1001, 3, "neg", "packed", "packed")]
+    bad = []
+    for it, ot, m, n, k, batch, am, bm, cm in cases:
+        res = []
+        plans = logged_plans(capfd, lambda: res.append(batched_case(  # noqa: B023
+            blas, it, ot, 1, 0, m, n, k, 1.0, 0.0, batch, am, bm, cm, seed=k)))
+        if res != [0] or len(plans) != 1 or plans[0]["copy_a"] != "1" or plans[0]["copy_b"] != "1":
+            bad.append((it, ot, m, n, k, batch, res, plans))
+    assert not bad, bad
+
+
 def test_batched_probe_capacity(blas):
     """A cycle probe must hold batchCount times one GemmEx's slots."""
     m = n = 256
