@@ -374,6 +374,10 @@ constexpr int kChunks = kFastKBytes / 16;
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
 
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+// gemm_tn128's [k][m] layout of an M-contiguous A: 16-byte chunk XOR for
+// k-row k of a stage.
+__device__ __forceinline__ int an_swz(int k) { return 2 * ((k & 3) | ((k >> 2) & 4)); }
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -924,9 +928,18 @@ __global__ __launch_bounds__(256, 1) void gemm_tn_fast(KParams batch_p) {
 // (8 or 16 bytes).
 constexpr int kT128 = 128;
 
-template <class Op, MmaOut OUT, int NS, bool STREAM = true>
+// AN: op(A) = A stored M-contiguous (transa = N, 16-bit inputs), read
+// without a transposed copy: its stage holds 64 k-rows of the tile's 128 m
+// ([k][m], 256 bytes a row, 16-byte chunks XOR-swizzled by 2 * ((k & 3) |
+// ((k >> 2) & 4))), each A fragment is two transposing reads
+// (ds_read_b64_tr_b16: a 16-lane group reads 4 k-rows x 16 m, each lane
+// receiving the 4 k of its m), at the same k chunk as the B fragment of its
+// lanes, so every product is unchanged; over the 32 lanes of a read cycle
+// the swizzle puts the 8 rows' 16 chunks on distinct banks.
+template <class Op, MmaOut OUT, int NS, bool STREAM = true, bool AN = false>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch_p) {
   static_assert(NS == 2 || NS == 4, "stages in the ring: 4 (one workgroup per CU) or 2 (two)");
+  static_assert(!AN || Op::kElemBytes == 2, "M-contiguous A: 16-bit inputs only");
   constexpr uint32_t kStage = kT128 * kChunks * 16;       // 16 KB per operand and stage
   const KParams p = batch_view(batch_p);
   // [A | B][stage][row * 8 + physical chunk], 16 bytes per entry.
@@ -948,6 +961,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
   const int rows_a = min(kT128, p.m - row0);
   const int rows_b = min(kT128, p.n - col0);
   constexpr uint32_t kOff = 0x80000000u;
+  constexpr int kRowsAN = kFastKBytes / 2;                // k-rows of an AN stage (64)
   auto rsrc_words = [&](const uint8_t* base, int bytes) {
     const uint64_t a = (uint64_t)(uintptr_t)base;
     i32x4 r;
@@ -957,7 +971,11 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     r[3] = (int)kRsrcWord3;
     return r;
   };
-  const i32x4 rsa = rsrc_words(p.a + (int64_t)row0 * lda_b, (rows_a - 1) * lda_b + kbytes);
+  // AN: from the tile's first m; every k-row of A, to the end of the matrix
+  // (m past the matrix within a row reads the next row's values, which only
+  // reach rows of C that are never stored).
+  const i32x4 rsa = AN ? rsrc_words(p.a + (int64_t)row0 * 2, (p.k - 1) * lda_b + (p.m - row0) * 2)
+                       : rsrc_words(p.a + (int64_t)row0 * lda_b, (rows_a - 1) * lda_b + kbytes);
   const i32x4 rsb = rsrc_words(p.b + (int64_t)col0 * ldb_b, (rows_b - 1) * ldb_b + kbytes);
   // DMA instruction d (0..7) of a stage: operand d / 4, the 1 KB block of
   // rows 8*(4*(d%4) + wave) .. +7, lane L landing in row +L/8 at physical
@@ -969,7 +987,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     const int blk = 4 * i + wave;
     const int row = 8 * blk + lr;
     const int c = pc ^ lr ^ (blk & 7);
-    base_a[i] = (uint32_t)(row * lda_b + 16 * c);
+    base_a[i] = AN ? (uint32_t)((4 * blk + (lane >> 4)) * lda_b +
+                                16 * ((lane & 15) ^ an_swz(4 * blk + (lane >> 4))))
+                   : (uint32_t)(row * lda_b + 16 * c);
     base_b[i] = (uint32_t)(row * ldb_b + 16 * c);
   }
   auto dma = [&](int kt, int st, int d) __attribute__((always_inline)) {
@@ -980,7 +1000,14 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     const bool ok = kt < ktiles && kb + 16 * c < kbytes;
     // One wait state between the M0 write and the DMA that reads it (the
     // hazard pass does not look inside inline assembly).
-    if (d < 4) {
+    if (d < 4 && AN) {
+      // 4 k-rows of 256 bytes: lane L -> row 4*blk + L/16, physical chunk L%16
+      const int krow = kt * kRowsAN + 4 * blk + (lane >> 4);
+      const uint32_t v = krow < p.k ? base_a[i] + (uint32_t)(kt * kRowsAN) * (uint32_t)lda_b : kOff;
+      const uint32_t l = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][st][blk * 64];
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                   :: "s"(l), "v"(v), "s"(rsa) : "memory");
+    } else if (d < 4) {
       const uint32_t v = ok ? base_a[i] + (uint32_t)kb : kOff;
       const uint32_t l = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][st][blk * 64];
       asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
@@ -1018,6 +1045,31 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
       ad_a[t][ks] = lds0 + 16u * (uint32_t)(ar * kChunks + (kc ^ swz(ar)));
       ad_b[t][ks] = lds0 + NS * kStage + 16u * (uint32_t)(br * kChunks + (kc ^ swz(br)));
     }
+  // AN: per A tile and k-step, the two transposing reads' addresses (k-rows
+  // 8c .. 8c+3 and 8c+4 .. 8c+7 of chunk c = 4*ks + kq, m = 16t + 4*(j&3)
+  // for lane j of its 16-lane group).
+  uint32_t ad_an[AN ? 4 : 1][2][2];
+  if constexpr (AN) {
+    const int j = lane & 15;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int krow = 8 * (4 * ks + kq) + 4 * h + (j >> 2);
+          const int m = wm * 64 + 16 * t + 4 * (j & 3);
+          ad_an[t][ks][h] = lds0 + 256u * (uint32_t)krow + 16u * (uint32_t)((m >> 3) ^ an_swz(krow)) +
+                            2u * (uint32_t)(m & 7);
+        }
+  }
+  typedef __attribute__((address_space(3))) s16x4* lds_s16x4_t;
+  auto frag_an = [&](int t, int rks, uint32_t off) __attribute__((always_inline)) -> i32x4 {
+    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad_an[AN ? t : 0][rks][0] + off));
+    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad_an[AN ? t : 0][rks][1] + off));
+    const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+    return i32x4{(int)w0.x, (int)w0.y, (int)w1.x, (int)w1.y};
+  };
   i32x4 fa[2][4], fb[2][4];
   // One k-step: 16 MFMAs (A tile q/4 x B tile q%4). Behind the odd slots,
   // the next k-step's 8 fragments (stage offset `off`, k-step `rks`) into
@@ -1034,7 +1086,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
       __builtin_amdgcn_sched_barrier(0);
       if (q & 1) {
         const int f = q >> 1;
-        if (f < 4) fa[buf ^ 1][f] = *(lds_frag_t)(uintptr_t)(ad_a[f][rks] + off);
+        if (f < 4 && AN) fa[buf ^ 1][f] = frag_an(f, rks, off);
+        else if (f < 4) fa[buf ^ 1][f] = *(lds_frag_t)(uintptr_t)(ad_a[f][rks] + off);
         else fb[buf ^ 1][f - 4] = *(lds_frag_t)(uintptr_t)(ad_b[f - 4][rks] + off);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1053,7 +1106,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    fa[0][t] = *(lds_frag_t)(uintptr_t)ad_a[t][0];
+    fa[0][t] = AN ? frag_an(t, 0, 0) : *(lds_frag_t)(uintptr_t)ad_a[t][0];
     fb[0][t] = *(lds_frag_t)(uintptr_t)ad_b[t][0];
   }
   for (int kt = 0; kt < ktiles; ++kt) {
@@ -1435,6 +1488,7 @@ struct Plan {
   int64_t split_ns = 0;           // the split's modelled time (fp32 problems of 256+ tiles)
   bool tn128 = false;             // the TN problem runs on 128x128 tiles (gemm_tn128)
   int tn128_stages = 4;           // its LDS ring: 4 stages (one workgroup per CU) or 2 (two)
+  bool a_direct = false;          // gemm_tn128 reads a 16-bit A (transa N) where it lies
   GemmDesc e;                     // the TN problem (over the copies; ws unset)
   size_t bytes() const { return a_bytes + b_bytes + w_bytes; }
 };
@@ -1631,10 +1685,38 @@ bool c_ready(const GemmDesc& d) {
   return (d.ldc * OB) % 16 == 0 && ((uintptr_t)d.c % 16) == 0 && (d.stride_c * OB) % 16 == 0;
 }
 
+// A 16-bit op(A) = A (transa N, M-contiguous) on one pass of gemm_tn128 is
+// read where it lies, through transposing LDS reads, instead of through a
+// transposed copy (bf16 N,N 2048^3: 540 TFLOP/s behind the copy).
+template <class Op>
+Plan direct_a(const GemmDesc& d, Plan t) {
+  if (Op::kElemBytes != 2 || !t.tn || !t.tn128 || t.split > 1 || t.c_staged || !t.copy_a ||
+      t.copy_b || t.kp != d.k)
+    return t;
+  // 16-byte chunks of m: m a multiple of 8, so that no chunk straddles the
+  // end of the matrix (whose buffer record ends at the last element) and
+  // every chunk holding valid values is read whole; DMA offsets within the
+  // 2^31 bytes a buffer offset reaches below the zero-fill offset (the last
+  // k-row, plus a 128-row stage of slack).
+  if (d.m % 8 != 0 || (uintptr_t)d.a % 16 != 0 || (d.lda * 2) % 16 != 0 || (d.stride_a * 2) % 16 != 0 ||
+      ((int64_t)d.k + kT128) * d.lda * 2 >= (1ll << 31))
+    return t;
+  t.copy_a = false;
+  t.a_direct = true;
+  t.batch_a = 0;
+  t.a_bytes = 0;
+  t.e.a = d.a;
+  t.e.ta = false;
+  t.e.lda = d.lda;
+  t.e.stride_a = d.stride_a;
+  return t;
+}
+
 template <class Op, MmaOut OUT>
 Plan make_plan(const GemmDesc& d) {
   Plan t = make_plan_core<Op, OUT>(d);
-  if (t.tn || std::is_same<Op, OpF32>::value || d.batch != 1 || d.probe || !d.pad_copies ||
+  if (t.tn) return direct_a<Op>(d, t);
+  if (std::is_same<Op, OpF32>::value || d.batch != 1 || d.probe || !d.pad_copies ||
       d.k <= 0 || (int64_t)d.m * d.n * d.k < kTransposeMinWork || c_ready<OUT>(d))
     return t;
   GemmDesc q = d;
@@ -1719,10 +1801,11 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   if (log_plans()) {
     std::fprintf(stderr,
                  "grxblas: gemm %s->%s ta=%d tb=%d m=%d n=%d k=%d batch=%d kernel=%s copy_a=%d "
-                 "copy_b=%d split=%d ring=%d staged=%d\n",
+                 "copy_b=%d split=%d ring=%d staged=%d direct_a=%d\n",
                  Op::kName, out_name<OUT>(), (int)d.ta, (int)d.tb, d.m, d.n, d.k, d.batch,
                  t.tn ? (t.tn128 ? "tn128" : "tn256") : "general64", (int)t.copy_a, (int)t.copy_b, t.split,
-                 t.tn && t.tn128 ? t.tn128_stages : 0, (int)(t.tn && t.c_staged));
+                 t.tn && t.tn128 ? t.tn128_stages : 0, (int)(t.tn && t.c_staged),
+                 (int)(t.tn && t.a_direct));
   }
 
   KParams p{};
@@ -1783,6 +1866,17 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     p.tiles_n = (g->n + kT128 - 1) / kT128;
     if constexpr (Op::kM16)   // the plan takes this path for 16-bit and int8 inputs only
     {
+      if constexpr (Op::kElemBytes == 2) {
+        if (t.a_direct) {
+          if (t.tn128_stages == 2)
+            hipLaunchKernelGGL((gemm_tn128<Op, OUT, 2, true, true>), dim3(p.tiles_m * p.tiles_n, g->batch),
+                               dim3(256), 0, s, p);
+          else
+            hipLaunchKernelGGL((gemm_tn128<Op, OUT, 4, true, true>), dim3(p.tiles_m * p.tiles_n, g->batch),
+                               dim3(256), 0, s, p);
+          return hipGetLastError();
+        }
+      }
       if (t.tn128_stages == 2)
         hipLaunchKernelGGL((gemm_tn128<Op, OUT, 2>), dim3(p.tiles_m * p.tiles_n, g->batch), dim3(256), 0, s, p);
       else

@@ -242,9 +242,10 @@ def test_split_k_plan_limits(blas, capfd):
 def test_tn128_path_exact(blas, capfd):
     """16-bit and int8 problems of at least 1024 x 1024 with few 256x256 tiles
     and at most 32 stages of K run on 128x128 tiles: every input/output
-    type, (T, N) directly and (N, N) behind the operand copy, ragged m and
-    K, alpha/beta, bit-exact against the oracle over the whole padded C,
-    with guard bands; the GRXBLAS_LOG line shows the path taken."""
+    type, (T, N) directly and (N, N) with A read where it lies (16-bit) or
+    behind the operand copy (int8), ragged n and K, alpha/beta, bit-exact
+    against the oracle over the whole padded C, with guard bands; the
+    GRXBLAS_LOG line shows the path taken."""
     cases = []
     for ta, tb in ((1, 0), (0, 0)):
         for it, ot in ((BF16, F32), (BF16, BF16), (F16, F16), (F16, F32)):
@@ -267,9 +268,33 @@ def test_tn128_path_exact(blas, capfd):
             call = lambda: res.append(dequant_case(blas, ta, tb, m, n, k, 0, 8, seed=11, guard=True))
             ok = (0, 0)
         plans = logged_plans(capfd, call)
-        if res != [ok] or len(plans) != 1 or plans[0]["kernel"] != "tn128":
+        direct = "1" if kind == "f" and ta == 0 else "0"
+        if res != [ok] or len(plans) != 1 or plans[0]["kernel"] != "tn128" or \
+                plans[0]["direct_a"] != direct or plans[0]["copy_a"] != str(1 - ta - int(direct)):
             bad.append((kind, ta, tb, it, ot, res, plans))
     assert not bad, bad
+
+
+@pytest.mark.parametrize("it,ot,m,n,k,pad,alpha,beta,ring,direct", [
+    (BF16, BF16, 1032, 1100, 200, 8, 1.5, -0.5, "4", "1"),   # lda > m, K ends inside a stage
+    (F16, F32, 2176, 2176, 128, 0, 1.0, 0.0, "2", "1"),       # 289 tiles: the two-stage ring
+    (BF16, F32, 1024, 2048, 16, 0, 2.5, 1.0, "4", "1"),       # 16 k-rows: one stage, mostly zero fill
+    (F16, F16, 1096, 1024, 1000, 0, 1.0, 0.0, "4", "1"),      # 16 stages, the last one partial
+    (BF16, BF16, 1030, 1100, 200, 0, 1.0, 0.0, "4", "0"),     # lda = m = 1030: behind the copy
+])
+def test_direct_a_exact(blas, capfd, it, ot, m, n, k, pad, alpha, beta, ring, direct):
+    """16-bit (N, N) problems on one pass of the 128x128 kernel read A where
+    it lies (M-contiguous, k-rows of the tile's 128 m staged in LDS and read
+    through transposing reads), no copy of A: bit-exact over the padded C
+    with guard bands, both rings, K ending inside a stage, lda > m; A whose
+    columns are off 16-byte boundaries (lda = m = 1030) keeps the copy."""
+    res = []
+    plans = logged_plans(capfd, lambda: res.append(
+        float_case(blas, it, ot, 0, 0, m, n, k, alpha, beta, pad, (-m) % 8, seed=k + m, guard=True)))
+    assert res == [(0, 0)]
+    assert len(plans) == 1 and plans[0]["kernel"] == "tn128" and plans[0]["ring"] == ring, plans
+    assert plans[0]["direct_a"] == direct and plans[0]["copy_a"] == str(1 - int(direct)), plans
+    assert plans[0]["copy_b"] == "0" and plans[0]["split"] == "1", plans
 
 
 @pytest.mark.parametrize("kind,it,ot,m,n,k", [
