@@ -935,11 +935,12 @@ constexpr int kT128 = 128;
 // (ds_read_b64_tr_b16: a 16-lane group reads 4 k-rows x 16 m, each lane
 // receiving the 4 k of its m), at the same k chunk as the B fragment of its
 // lanes, so every product is unchanged; over the 32 lanes of a read cycle
-// the swizzle puts the 8 rows' 16 chunks on distinct banks.
-template <class Op, MmaOut OUT, int NS, bool STREAM = true, bool AN = false>
+// the swizzle puts the 8 rows' 16 chunks on distinct banks. BN: the same
+// for op(B) = B^T stored N-contiguous (transb = T).
+template <class Op, MmaOut OUT, int NS, bool STREAM = true, bool AN = false, bool BN = false>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch_p) {
   static_assert(NS == 2 || NS == 4, "stages in the ring: 4 (one workgroup per CU) or 2 (two)");
-  static_assert(!AN || Op::kElemBytes == 2, "M-contiguous A: 16-bit inputs only");
+  static_assert((!AN && !BN) || Op::kElemBytes == 2, "M/N-contiguous operands: 16-bit inputs only");
   constexpr uint32_t kStage = kT128 * kChunks * 16;       // 16 KB per operand and stage
   const KParams p = batch_view(batch_p);
   // [A | B][stage][row * 8 + physical chunk], 16 bytes per entry.
@@ -973,10 +974,11 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
   };
   // AN: from the tile's first m; every k-row of A, to the end of the matrix
   // (m past the matrix within a row reads the next row's values, which only
-  // reach rows of C that are never stored).
+  // reach rows of C that are never stored). BN likewise from the first n.
   const i32x4 rsa = AN ? rsrc_words(p.a + (int64_t)row0 * 2, (p.k - 1) * lda_b + (p.m - row0) * 2)
                        : rsrc_words(p.a + (int64_t)row0 * lda_b, (rows_a - 1) * lda_b + kbytes);
-  const i32x4 rsb = rsrc_words(p.b + (int64_t)col0 * ldb_b, (rows_b - 1) * ldb_b + kbytes);
+  const i32x4 rsb = BN ? rsrc_words(p.b + (int64_t)col0 * 2, (p.k - 1) * ldb_b + (p.n - col0) * 2)
+                       : rsrc_words(p.b + (int64_t)col0 * ldb_b, (rows_b - 1) * ldb_b + kbytes);
   // DMA instruction d (0..7) of a stage: operand d / 4, the 1 KB block of
   // rows 8*(4*(d%4) + wave) .. +7, lane L landing in row +L/8 at physical
   // chunk L%8 and fetching logical chunk (L%8) ^ swz(row).
@@ -990,7 +992,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     base_a[i] = AN ? (uint32_t)((4 * blk + (lane >> 4)) * lda_b +
                                 16 * ((lane & 15) ^ an_swz(4 * blk + (lane >> 4))))
                    : (uint32_t)(row * lda_b + 16 * c);
-    base_b[i] = (uint32_t)(row * ldb_b + 16 * c);
+    base_b[i] = BN ? (uint32_t)((4 * blk + (lane >> 4)) * ldb_b +
+                                16 * ((lane & 15) ^ an_swz(4 * blk + (lane >> 4))))
+                   : (uint32_t)(row * ldb_b + 16 * c);
   }
   auto dma = [&](int kt, int st, int d) __attribute__((always_inline)) {
     const int i = d & 3;
@@ -1000,13 +1004,18 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     const bool ok = kt < ktiles && kb + 16 * c < kbytes;
     // One wait state between the M0 write and the DMA that reads it (the
     // hazard pass does not look inside inline assembly).
-    if (d < 4 && AN) {
+    if ((d < 4 && AN) || (d >= 4 && BN)) {
       // 4 k-rows of 256 bytes: lane L -> row 4*blk + L/16, physical chunk L%16
       const int krow = kt * kRowsAN + 4 * blk + (lane >> 4);
-      const uint32_t v = krow < p.k ? base_a[i] + (uint32_t)(kt * kRowsAN) * (uint32_t)lda_b : kOff;
-      const uint32_t l = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][st][blk * 64];
-      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                   :: "s"(l), "v"(v), "s"(rsa) : "memory");
+      const uint32_t ld = (uint32_t)(d < 4 ? lda_b : ldb_b);
+      const uint32_t v = krow < p.k ? (d < 4 ? base_a[i] : base_b[i]) + (uint32_t)(kt * kRowsAN) * ld : kOff;
+      const uint32_t l = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[d < 4 ? 0 : 1][st][blk * 64];
+      if (d < 4)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                     :: "s"(l), "v"(v), "s"(rsa) : "memory");
+      else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                     :: "s"(l), "v"(v), "s"(rsb) : "memory");
     } else if (d < 4) {
       const uint32_t v = ok ? base_a[i] + (uint32_t)kb : kOff;
       const uint32_t l = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[0][st][blk * 64];
@@ -1045,11 +1054,11 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
       ad_a[t][ks] = lds0 + 16u * (uint32_t)(ar * kChunks + (kc ^ swz(ar)));
       ad_b[t][ks] = lds0 + NS * kStage + 16u * (uint32_t)(br * kChunks + (kc ^ swz(br)));
     }
-  // AN: per A tile and k-step, the two transposing reads' addresses (k-rows
-  // 8c .. 8c+3 and 8c+4 .. 8c+7 of chunk c = 4*ks + kq, m = 16t + 4*(j&3)
-  // for lane j of its 16-lane group).
-  uint32_t ad_an[AN ? 4 : 1][2][2];
-  if constexpr (AN) {
+  // AN / BN: per tile and k-step, the two transposing reads' addresses
+  // (k-rows 8c .. 8c+3 and 8c+4 .. 8c+7 of chunk c = 4*ks + kq, m (or n) =
+  // 16t + 4*(j&3) for lane j of its 16-lane group).
+  uint32_t ad_an[AN ? 4 : 1][2][2], ad_bn[BN ? 4 : 1][2][2];
+  auto tr_addrs = [&](uint32_t (*ad)[2][2], int w, uint32_t base) __attribute__((always_inline)) {
     const int j = lane & 15;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -1058,15 +1067,18 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int krow = 8 * (4 * ks + kq) + 4 * h + (j >> 2);
-          const int m = wm * 64 + 16 * t + 4 * (j & 3);
-          ad_an[t][ks][h] = lds0 + 256u * (uint32_t)krow + 16u * (uint32_t)((m >> 3) ^ an_swz(krow)) +
-                            2u * (uint32_t)(m & 7);
+          const int m = w * 64 + 16 * t + 4 * (j & 3);
+          ad[t][ks][h] = base + 256u * (uint32_t)krow + 16u * (uint32_t)((m >> 3) ^ an_swz(krow)) +
+                         2u * (uint32_t)(m & 7);
         }
-  }
+  };
+  if constexpr (AN) tr_addrs(ad_an, wm, lds0);
+  if constexpr (BN) tr_addrs(ad_bn, wn, lds0 + NS * kStage);
   typedef __attribute__((address_space(3))) s16x4* lds_s16x4_t;
-  auto frag_an = [&](int t, int rks, uint32_t off) __attribute__((always_inline)) -> i32x4 {
-    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad_an[AN ? t : 0][rks][0] + off));
-    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad_an[AN ? t : 0][rks][1] + off));
+  auto frag_tr = [&](const uint32_t (*ad)[2][2], int t, int rks, uint32_t off)
+      __attribute__((always_inline)) -> i32x4 {
+    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad[t][rks][0] + off));
+    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad[t][rks][1] + off));
     const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
     return i32x4{(int)w0.x, (int)w0.y, (int)w1.x, (int)w1.y};
   };
@@ -1086,8 +1098,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
       __builtin_amdgcn_sched_barrier(0);
       if (q & 1) {
         const int f = q >> 1;
-        if (f < 4 && AN) fa[buf ^ 1][f] = frag_an(f, rks, off);
+        if (f < 4 && AN) fa[buf ^ 1][f] = frag_tr(ad_an, f & (AN ? 3 : 0), rks, off);
         else if (f < 4) fa[buf ^ 1][f] = *(lds_frag_t)(uintptr_t)(ad_a[f][rks] + off);
+        else if (BN) fb[buf ^ 1][f - 4] = frag_tr(ad_bn, (f - 4) & (BN ? 3 : 0), rks, off);
         else fb[buf ^ 1][f - 4] = *(lds_frag_t)(uintptr_t)(ad_b[f - 4][rks] + off);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1106,8 +1119,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    fa[0][t] = AN ? frag_an(t, 0, 0) : *(lds_frag_t)(uintptr_t)ad_a[t][0];
-    fb[0][t] = *(lds_frag_t)(uintptr_t)ad_b[t][0];
+    fa[0][t] = AN ? frag_tr(ad_an, t & (AN ? 3 : 0), 0, 0) : *(lds_frag_t)(uintptr_t)ad_a[t][0];
+    fb[0][t] = BN ? frag_tr(ad_bn, t & (BN ? 3 : 0), 0, 0) : *(lds_frag_t)(uintptr_t)ad_b[t][0];
   }
   for (int kt = 0; kt < ktiles; ++kt) {
     const int st = kt & (NS - 1);
@@ -1489,6 +1502,7 @@ struct Plan {
   bool tn128 = false;             // the TN problem runs on 128x128 tiles (gemm_tn128)
   int tn128_stages = 4;           // its LDS ring: 4 stages (one workgroup per CU) or 2 (two)
   bool a_direct = false;          // gemm_tn128 reads a 16-bit A (transa N) where it lies
+  bool b_direct = false;          // ... and a 16-bit B (transb T)
   GemmDesc e;                     // the TN problem (over the copies; ws unset)
   size_t bytes() const { return a_bytes + b_bytes + w_bytes; }
 };
@@ -1685,37 +1699,50 @@ bool c_ready(const GemmDesc& d) {
   return (d.ldc * OB) % 16 == 0 && ((uintptr_t)d.c % 16) == 0 && (d.stride_c * OB) % 16 == 0;
 }
 
-// A 16-bit op(A) = A (transa N, M-contiguous) on one pass of gemm_tn128 is
-// read where it lies, through transposing LDS reads, instead of through a
-// transposed copy (bf16 N,N 2048^3: 540 TFLOP/s behind the copy).
+// A 16-bit op(A) = A (transa N, M-contiguous) or op(B) = B^T (transb T,
+// N-contiguous) on one pass of gemm_tn128 is read where it lies, through
+// transposing LDS reads, instead of through a transposed copy (bf16 N,N
+// 2048^3: 540 TFLOP/s behind the copy, 643-681 without).
+// 16-byte chunks of m (n): m (n) a multiple of 8, so that no chunk straddles
+// the end of the matrix (whose buffer record ends at the last element) and
+// every chunk holding valid values is read whole; DMA offsets within the
+// 2^31 bytes a buffer offset reaches below the zero-fill offset (the last
+// k-row, plus a 128-row stage of slack).
+inline bool direct_ok(int rows, const void* x, int64_t ld, int64_t stride, int k) {
+  return rows % 8 == 0 && (uintptr_t)x % 16 == 0 && (ld * 2) % 16 == 0 && (stride * 2) % 16 == 0 &&
+         ((int64_t)k + kT128) * ld * 2 < (1ll << 31);
+}
+
 template <class Op>
-Plan direct_a(const GemmDesc& d, Plan t) {
-  if (Op::kElemBytes != 2 || !t.tn || !t.tn128 || t.split > 1 || t.c_staged || !t.copy_a ||
-      t.copy_b || t.kp != d.k)
-    return t;
-  // 16-byte chunks of m: m a multiple of 8, so that no chunk straddles the
-  // end of the matrix (whose buffer record ends at the last element) and
-  // every chunk holding valid values is read whole; DMA offsets within the
-  // 2^31 bytes a buffer offset reaches below the zero-fill offset (the last
-  // k-row, plus a 128-row stage of slack).
-  if (d.m % 8 != 0 || (uintptr_t)d.a % 16 != 0 || (d.lda * 2) % 16 != 0 || (d.stride_a * 2) % 16 != 0 ||
-      ((int64_t)d.k + kT128) * d.lda * 2 >= (1ll << 31))
-    return t;
-  t.copy_a = false;
-  t.a_direct = true;
-  t.batch_a = 0;
-  t.a_bytes = 0;
-  t.e.a = d.a;
-  t.e.ta = false;
-  t.e.lda = d.lda;
-  t.e.stride_a = d.stride_a;
+Plan direct_operands(const GemmDesc& d, Plan t) {
+  if (Op::kElemBytes != 2 || !t.tn || !t.tn128 || t.split > 1 || t.c_staged || t.kp != d.k) return t;
+  if (t.copy_a && !d.ta && direct_ok(d.m, d.a, d.lda, d.stride_a, d.k)) {
+    t.copy_a = false;
+    t.a_direct = true;
+    t.batch_a = 0;
+    t.a_bytes = 0;
+    t.e.a = d.a;
+    t.e.ta = false;
+    t.e.lda = d.lda;
+    t.e.stride_a = d.stride_a;
+  }
+  if (t.copy_b && d.tb && direct_ok(d.n, d.b, d.ldb, d.stride_b, d.k)) {
+    t.copy_b = false;
+    t.b_direct = true;
+    t.batch_b = 0;
+    t.b_bytes = 0;
+    t.e.b = d.b;
+    t.e.tb = true;
+    t.e.ldb = d.ldb;
+    t.e.stride_b = d.stride_b;
+  }
   return t;
 }
 
 template <class Op, MmaOut OUT>
 Plan make_plan(const GemmDesc& d) {
   Plan t = make_plan_core<Op, OUT>(d);
-  if (t.tn) return direct_a<Op>(d, t);
+  if (t.tn) return direct_operands<Op>(d, t);
   if (std::is_same<Op, OpF32>::value || d.batch != 1 || d.probe || !d.pad_copies ||
       d.k <= 0 || (int64_t)d.m * d.n * d.k < kTransposeMinWork || c_ready<OUT>(d))
     return t;
@@ -1801,11 +1828,11 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
   if (log_plans()) {
     std::fprintf(stderr,
                  "grxblas: gemm %s->%s ta=%d tb=%d m=%d n=%d k=%d batch=%d kernel=%s copy_a=%d "
-                 "copy_b=%d split=%d ring=%d staged=%d direct_a=%d\n",
+                 "copy_b=%d split=%d ring=%d staged=%d direct_a=%d direct_b=%d\n",
                  Op::kName, out_name<OUT>(), (int)d.ta, (int)d.tb, d.m, d.n, d.k, d.batch,
                  t.tn ? (t.tn128 ? "tn128" : "tn256") : "general64", (int)t.copy_a, (int)t.copy_b, t.split,
                  t.tn && t.tn128 ? t.tn128_stages : 0, (int)(t.tn && t.c_staged),
-                 (int)(t.tn && t.a_direct));
+                 (int)(t.tn && t.a_direct), (int)(t.tn && t.b_direct));
   }
 
   KParams p{};
@@ -1867,13 +1894,17 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     if constexpr (Op::kM16)   // the plan takes this path for 16-bit and int8 inputs only
     {
       if constexpr (Op::kElemBytes == 2) {
-        if (t.a_direct) {
-          if (t.tn128_stages == 2)
-            hipLaunchKernelGGL((gemm_tn128<Op, OUT, 2, true, true>), dim3(p.tiles_m * p.tiles_n, g->batch),
-                               dim3(256), 0, s, p);
-          else
-            hipLaunchKernelGGL((gemm_tn128<Op, OUT, 4, true, true>), dim3(p.tiles_m * p.tiles_n, g->batch),
-                               dim3(256), 0, s, p);
+        if (t.a_direct || t.b_direct) {
+          const dim3 grid(p.tiles_m * p.tiles_n, g->batch);
+          const int v = (t.tn128_stages == 2 ? 4 : 0) + (t.a_direct ? 1 : 0) + (t.b_direct ? 2 : 0);
+          switch (v) {
+            case 1: hipLaunchKernelGGL((gemm_tn128<Op, OUT, 4, true, true, false>), grid, dim3(256), 0, s, p); break;
+            case 2: hipLaunchKernelGGL((gemm_tn128<Op, OUT, 4, true, false, true>), grid, dim3(256), 0, s, p); break;
+            case 3: hipLaunchKernelGGL((gemm_tn128<Op, OUT, 4, true, true, true>), grid, dim3(256), 0, s, p); break;
+            case 5: hipLaunchKernelGGL((gemm_tn128<Op, OUT, 2, true, true, false>), grid, dim3(256), 0, s, p); break;
+            case 6: hipLaunchKernelGGL((gemm_tn128<Op, OUT, 2, true, false, true>), grid, dim3(256), 0, s, p); break;
+            default: hipLaunchKernelGGL((gemm_tn128<Op, OUT, 2, true, true, true>), grid, dim3(256), 0, s, p); break;
+          }
           return hipGetLastError();
         }
       }

@@ -275,26 +275,33 @@ def test_tn128_path_exact(blas, capfd):
     assert not bad, bad
 
 
-@pytest.mark.parametrize("it,ot,m,n,k,pad,alpha,beta,ring,direct", [
-    (BF16, BF16, 1032, 1100, 200, 8, 1.5, -0.5, "4", "1"),   # lda > m, K ends inside a stage
-    (F16, F32, 2176, 2176, 128, 0, 1.0, 0.0, "2", "1"),       # 289 tiles: the two-stage ring
-    (BF16, F32, 1024, 2048, 16, 0, 2.5, 1.0, "4", "1"),       # 16 k-rows: one stage, mostly zero fill
-    (F16, F16, 1096, 1024, 1000, 0, 1.0, 0.0, "4", "1"),      # 16 stages, the last one partial
-    (BF16, BF16, 1030, 1100, 200, 0, 1.0, 0.0, "4", "0"),     # lda = m = 1030: behind the copy
+@pytest.mark.parametrize("it,ot,ta,tb,m,n,k,pad,alpha,beta,ring,direct", [
+    (BF16, BF16, 0, 0, 1032, 1100, 200, 8, 1.5, -0.5, "4", "10"),  # lda > m, K ends inside a stage
+    (F16, F32, 0, 0, 2176, 2176, 128, 0, 1.0, 0.0, "2", "10"),     # 289 tiles: the two-stage ring
+    (BF16, F32, 0, 0, 1024, 2048, 16, 0, 2.5, 1.0, "4", "10"),     # 16 k-rows: one stage, mostly zero fill
+    (F16, F16, 0, 0, 1096, 1024, 1000, 0, 1.0, 0.0, "4", "10"),    # 16 stages, the last one partial
+    (BF16, BF16, 0, 0, 1030, 1100, 200, 0, 1.0, 0.0, "4", "00"),   # lda = m = 1030: behind the copy
+    (BF16, BF16, 1, 1, 1100, 1032, 200, 8, 1.5, -0.5, "4", "01"),  # op(B) = B^T read in place
+    (F16, F32, 0, 1, 1032, 1096, 1000, 0, 2.0, 1.0, "4", "11"),    # both in place
+    (BF16, F32, 0, 1, 2176, 2176, 128, 0, 1.0, 0.0, "2", "11"),    # both, the two-stage ring
+    (F16, F16, 0, 1, 1024, 1030, 200, 0, 1.0, 0.0, "4", "10"),     # ldb = n = 1030: B behind the copy
 ])
-def test_direct_a_exact(blas, capfd, it, ot, m, n, k, pad, alpha, beta, ring, direct):
-    """16-bit (N, N) problems on one pass of the 128x128 kernel read A where
-    it lies (M-contiguous, k-rows of the tile's 128 m staged in LDS and read
-    through transposing reads), no copy of A: bit-exact over the padded C
-    with guard bands, both rings, K ending inside a stage, lda > m; A whose
-    columns are off 16-byte boundaries (lda = m = 1030) keeps the copy."""
+def test_direct_operands_exact(blas, capfd, it, ot, ta, tb, m, n, k, pad, alpha, beta, ring, direct):
+    """16-bit problems on one pass of the 128x128 kernel read an M-contiguous
+    A (transa N) and an N-contiguous B (transb T) where they lie (k-rows of
+    the tile's 128 m or n staged in LDS and read through transposing reads),
+    with no copy: bit-exact over the padded C with guard bands, both rings, K
+    ending inside a stage, leading dimensions above m and n, alpha/beta, fp32
+    and 16-bit C; an operand whose columns are off 16-byte boundaries keeps
+    its copy. `direct` is the plan's (direct_a, direct_b)."""
     res = []
     plans = logged_plans(capfd, lambda: res.append(
-        float_case(blas, it, ot, 0, 0, m, n, k, alpha, beta, pad, (-m) % 8, seed=k + m, guard=True)))
+        float_case(blas, it, ot, ta, tb, m, n, k, alpha, beta, pad, (-m) % 8, seed=k + m, guard=True)))
     assert res == [(0, 0)]
     assert len(plans) == 1 and plans[0]["kernel"] == "tn128" and plans[0]["ring"] == ring, plans
-    assert plans[0]["direct_a"] == direct and plans[0]["copy_a"] == str(1 - int(direct)), plans
-    assert plans[0]["copy_b"] == "0" and plans[0]["split"] == "1", plans
+    p = plans[0]
+    assert p["direct_a"] + p["direct_b"] == direct and p["split"] == "1", plans
+    assert p["copy_a"] == str(1 - ta - int(direct[0])) and p["copy_b"] == str(tb - int(direct[1])), plans
 
 
 @pytest.mark.parametrize("kind,it,ot,m,n,k", [

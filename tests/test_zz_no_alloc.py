@@ -67,8 +67,9 @@ def test_noalloc_matches_gemm_ex_on_two_calls_in_a_row(blas, capfd):
     c1, c2, p1, p2 = _pair(blas, capfd, 1, 0, 1024, 1024, 8192, BF16, BF16, seed=1)
     assert p1 == p2 and len(p2) == 1 and int(p2[0]["split"]) > 1, (p1, p2)
     assert np.array_equal(c1.view(np.uint16), c2.view(np.uint16))
-    # 2: smaller, (T, T) -> the transposed copy of B in the scratch, fp32 C
-    c1, c2, p1, p2 = _pair(blas, capfd, 1, 1, 768, 512, 2048, BF16, F32, seed=2)
+    # 2: smaller, (T, T) with n = 508 (B's columns off 16 bytes, so not read
+    #    in place) -> the transposed copy of B in the scratch, fp32 C
+    c1, c2, p1, p2 = _pair(blas, capfd, 1, 1, 768, 508, 2048, BF16, F32, seed=2)
     assert p1 == p2 and len(p2) == 1 and p2[0]["copy_b"] == "1", (p1, p2)
     assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32))
 
