@@ -1702,7 +1702,14 @@ bool c_ready(const GemmDesc& d) {
 // A 16-bit op(A) = A (transa N, M-contiguous) or op(B) = B^T (transb T,
 // N-contiguous) on one pass of gemm_tn128 is read where it lies, through
 // transposing LDS reads, instead of through a transposed copy (bf16 N,N
-// 2048^3: 540 TFLOP/s behind the copy, 643-681 without).
+// 2048^3: 540 TFLOP/s behind the copy, 643-681 without). The 256x256
+// kernel keeps the copies: read in place there (the same layout at 512-byte
+// k-rows), bf16 N,N 8192^3 ran at 730 TFLOP/s against 1334 behind the copy,
+// and at 4096^3 its waves waited 14x as long (SQ_WAIT_ANY) with no more LDS
+// bank conflicts: every workgroup reads the same 64 k-rows of A per stage,
+// one 512 KB (4096^2) or 1 MB (8192^2) window of HBM at a time, where the
+// K-contiguous copy spreads a stage over the whole matrix, and its
+// two-stage ring has one stage of cover against the 128x128 kernel's three.
 // 16-byte chunks of m (n): m (n) a multiple of 8, so that no chunk straddles
 // the end of the matrix (whose buffer record ends at the last element) and
 // every chunk holding valid values is read whole; DMA offsets within the
@@ -1710,7 +1717,7 @@ bool c_ready(const GemmDesc& d) {
 // k-row, plus a 128-row stage of slack).
 inline bool direct_ok(int rows, const void* x, int64_t ld, int64_t stride, int k) {
   return rows % 8 == 0 && (uintptr_t)x % 16 == 0 && (ld * 2) % 16 == 0 && (stride * 2) % 16 == 0 &&
-         ((int64_t)k + kT128) * ld * 2 < (1ll << 31);
+         ((int64_t)k + kT128) * ld * 2 + 4096 < (1ll << 31);
 }
 
 template <class Op>

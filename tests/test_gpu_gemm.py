@@ -285,12 +285,15 @@ def test_tn128_path_exact(blas, capfd):
     (F16, F32, 0, 1, 1032, 1096, 1000, 0, 2.0, 1.0, "4", "11"),    # both in place
     (BF16, F32, 0, 1, 2176, 2176, 128, 0, 1.0, 0.0, "2", "11"),    # both, the two-stage ring
     (F16, F16, 0, 1, 1024, 1030, 200, 0, 1.0, 0.0, "4", "10"),     # ldb = n = 1030: B behind the copy
+    # 576 tiles of 128x128: the 256x256 kernel (ring 0) keeps the copies
+    (BF16, BF16, 0, 0, 3072, 3080, 64, 8, 1.5, -0.5, "0", "00"),
+    (F16, F32, 0, 1, 3080, 3072, 200, 0, 1.0, 0.0, "0", "00"),
 ])
 def test_direct_operands_exact(blas, capfd, it, ot, ta, tb, m, n, k, pad, alpha, beta, ring, direct):
     """16-bit problems on one pass of the 128x128 kernel read an M-contiguous
     A (transa N) and an N-contiguous B (transb T) where they lie (k-rows of
     the tile's 128 m or n staged in LDS and read through transposing reads),
-    with no copy: bit-exact over the padded C with guard bands, both rings, K
+    with no copy (the 256x256 kernel keeps the copies): bit-exact over the padded C with guard bands, both rings, K
     ending inside a stage, leading dimensions above m and n, alpha/beta, fp32
     and 16-bit C; an operand whose columns are off 16-byte boundaries keeps
     its copy. `direct` is the plan's (direct_a, direct_b)."""
@@ -298,7 +301,8 @@ def test_direct_operands_exact(blas, capfd, it, ot, ta, tb, m, n, k, pad, alpha,
     plans = logged_plans(capfd, lambda: res.append(
         float_case(blas, it, ot, ta, tb, m, n, k, alpha, beta, pad, (-m) % 8, seed=k + m, guard=True)))
     assert res == [(0, 0)]
-    assert len(plans) == 1 and plans[0]["kernel"] == "tn128" and plans[0]["ring"] == ring, plans
+    kernel = "tn256" if ring == "0" else "tn128"
+    assert len(plans) == 1 and plans[0]["kernel"] == kernel and plans[0]["ring"] == ring, plans
     p = plans[0]
     assert p["direct_a"] + p["direct_b"] == direct and p["split"] == "1", plans
     assert p["copy_a"] == str(1 - ta - int(direct[0])) and p["copy_b"] == str(tb - int(direct[1])), plans

@@ -85,16 +85,17 @@ def test_noalloc_int8_and_no_scratch_plans(blas, capfd):
 
 
 def test_noalloc_refuses_more_scratch_than_it_holds(blas, capfd):
-    """(N, N) 4096 x 4096 x 8200 bf16 would copy A (4096 x 8200 bf16, 67 MB)
-    into more than the 64 MiB scratch: NOT_SUPPORTED with a message, nothing
-    launched, C untouched. The buffers are full size, so nothing could
-    fault even if a launch happened."""
-    m, n, k = 4096, 4096, 8200
+    """(T, T) 4096 x 4092 x 8208 bf16 (B's columns, ldb = n = 4092, off 16
+    bytes, so B is not read in place) would copy B (4092 x 8208 bf16, 67.2
+    MB) into more than the 64 MiB scratch: NOT_SUPPORTED with a message,
+    nothing launched, C untouched. The buffers are full size, so nothing
+    could fault even if a launch happened."""
+    m, n, k = 4096, 4092, 8208
     dA, dB = g.DeviceBuffer(m * k * 2), g.DeviceBuffer(k * n * 2)
     poison = np.full(m * n, 0x7FC00001, np.uint32)
     dC = to_dev(poison)
     capfd.readouterr()
-    s = blas.gemm_ex_noalloc(0, 0, m, n, k, 1.0, dA.p, BF16, m, dB.p, BF16, k, 0.0, dC.p, F32, m)
+    s = blas.gemm_ex_noalloc(1, 1, m, n, k, 1.0, dA.p, BF16, k, dB.p, BF16, n, 0.0, dC.p, F32, m)
     err = capfd.readouterr().err
     g.synchronize()
     assert s == g.NOT_SUPPORTED, g.STATUS[s]
