@@ -1700,7 +1700,8 @@ bool c_ready(const GemmDesc& d) {
 }
 
 // A 16-bit op(A) = A (transa N, M-contiguous) or op(B) = B^T (transb T,
-// N-contiguous) on one pass of gemm_tn128 is read where it lies, through
+// N-contiguous) on gemm_tn128 (one pass, its K slices, or a staged C) is
+// read where it lies, through
 // transposing LDS reads, instead of through a transposed copy (bf16 N,N
 // 2048^3: 540 TFLOP/s behind the copy, 643-681 without). The 256x256
 // kernel keeps the copies: read in place there (the same layout at 512-byte
@@ -1722,7 +1723,7 @@ inline bool direct_ok(int rows, const void* x, int64_t ld, int64_t stride, int k
 
 template <class Op>
 Plan direct_operands(const GemmDesc& d, Plan t) {
-  if (Op::kElemBytes != 2 || !t.tn || !t.tn128 || t.split > 1 || t.c_staged || t.kp != d.k) return t;
+  if (Op::kElemBytes != 2 || !t.tn || !t.tn128 || t.kp != d.k) return t;
   if (t.copy_a && !d.ta && direct_ok(d.m, d.a, d.lda, d.stride_a, d.k)) {
     t.copy_a = false;
     t.a_direct = true;
@@ -1770,7 +1771,7 @@ Plan make_plan(const GemmDesc& d) {
     c.ldw = ((int64_t)d.m + 7) / 8 * 8;
     c.w_bytes = round256((size_t)c.ldw * d.n * 4);
   }
-  return c;
+  return direct_operands<Op>(d, c);
 }
 
 // GRXBLAS_LOG set (and not "0"): one line on stderr per GemmEx-family call
@@ -1867,8 +1868,10 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     q.ldc = t.ldw;
     q.k = t.kslice;
     q.k_last = t.k_last;
-    q.sa = (int64_t)t.kslice * EB;
-    q.sb = (int64_t)t.kslice * EB;
+    // slice z starts kslice elements down K: along a row of the TN layout,
+    // kslice rows down an operand read in place
+    q.sa = (int64_t)t.kslice * EB * (t.a_direct ? g->lda : 1);
+    q.sb = (int64_t)t.kslice * EB * (t.b_direct ? g->ldb : 1);
     q.sc = t.ldw * g->n * 4;
     q.alpha = 1.0f; q.beta = 0.0f; q.ialpha = 1; q.ibeta = 0;
     q.scale = nullptr;
@@ -1877,12 +1880,23 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
       if (t.tn128) {                  // slices on 128x128 tiles
         q.tiles_m = (g->m + kT128 - 1) / kT128;
         q.tiles_n = (g->n + kT128 - 1) / kT128;
-        if (t.tn128_stages == 2)
-          hipLaunchKernelGGL((gemm_tn128<Op, RAW, 2, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256),
-                             0, s, q);
-        else
-          hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false>), dim3(q.tiles_m * q.tiles_n, t.split), dim3(256),
-                             0, s, q);
+        const dim3 grid(q.tiles_m * q.tiles_n, t.split);
+        const int v = (t.tn128_stages == 2 ? 4 : 0) + (t.a_direct ? 1 : 0) + (t.b_direct ? 2 : 0);
+        if constexpr (Op::kElemBytes == 2) {      // operands read in place: 16-bit only
+          switch (v) {
+            case 1: hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false, true, false>), grid, dim3(256), 0, s, q); break;
+            case 2: hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false, false, true>), grid, dim3(256), 0, s, q); break;
+            case 3: hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false, true, true>), grid, dim3(256), 0, s, q); break;
+            case 5: hipLaunchKernelGGL((gemm_tn128<Op, RAW, 2, false, true, false>), grid, dim3(256), 0, s, q); break;
+            case 6: hipLaunchKernelGGL((gemm_tn128<Op, RAW, 2, false, false, true>), grid, dim3(256), 0, s, q); break;
+            case 7: hipLaunchKernelGGL((gemm_tn128<Op, RAW, 2, false, true, true>), grid, dim3(256), 0, s, q); break;
+            default: break;
+          }
+        }
+        if (v == 4)
+          hipLaunchKernelGGL((gemm_tn128<Op, RAW, 2, false>), grid, dim3(256), 0, s, q);
+        else if (v == 0)
+          hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false>), grid, dim3(256), 0, s, q);
       }
     }
     if (!t.tn128) {

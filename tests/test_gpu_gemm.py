@@ -215,7 +215,9 @@ def test_split_k_after_transposed_copies(blas, capfd, ta, tb):
         float_case(blas, BF16, BF16, ta, tb, 512, 256, 4096, 1.0, 0.0, 0)))
     assert res == [(0, 0)]
     p = plans[0]
-    assert (p["copy_a"], p["copy_b"]) == (str(1 - ta), str(tb)) and int(p["split"]) >= 2, plans
+    # the 16-bit operand stored M- (N-) contiguous is read in place by the slices
+    assert (p["direct_a"], p["direct_b"]) == (str(1 - ta), str(tb)) and int(p["split"]) >= 2, plans
+    assert (p["copy_a"], p["copy_b"]) == ("0", "0"), plans
 
 
 def test_split_k_plan_limits(blas, capfd):
@@ -306,6 +308,28 @@ def test_direct_operands_exact(blas, capfd, it, ot, ta, tb, m, n, k, pad, alpha,
     p = plans[0]
     assert p["direct_a"] + p["direct_b"] == direct and p["split"] == "1", plans
     assert p["copy_a"] == str(1 - ta - int(direct[0])) and p["copy_b"] == str(tb - int(direct[1])), plans
+
+
+@pytest.mark.parametrize("it,ot,ta,tb,m,n,k,cpad,split,staged,direct", [
+    (BF16, F32, 0, 0, 512, 256, 4096, 0, True, "0", "10"),     # K slices
+    (F16, F16, 1, 1, 512, 264, 4096, 0, True, "0", "01"),
+    (BF16, BF16, 0, 1, 1024, 1024, 1000, 1, False, "1", "11"),  # ldc = 1025: C staged, one slice
+    (F16, F32, 0, 0, 1024, 512, 8192, 1, True, "1", "10"),      # C staged behind K slices
+])
+def test_direct_operands_with_slices_and_staged_c(blas, capfd, it, ot, ta, tb, m, n, k, cpad, split,
+                                                   staged, direct):
+    """The 128x128 kernel's K slices (each slice reading its k-rows of an
+    operand in place, kslice rows down) and its staged C (raw partials, then
+    the epilogue into an unaligned C) with in-place operands: bit-exact over
+    the padded C with guard bands, no copy in the plan."""
+    res = []
+    plans = logged_plans(capfd, lambda: res.append(
+        float_case(blas, it, ot, ta, tb, m, n, k, 1.5, -0.5, 0, cpad, seed=k + m, guard=True)))
+    assert res == [(0, 0)]
+    p = plans[0]
+    assert len(plans) == 1 and p["kernel"] == "tn128" and (int(p["split"]) > 1) == split, plans
+    assert p["staged"] == staged and p["direct_a"] + p["direct_b"] == direct, plans
+    assert (p["copy_a"], p["copy_b"]) == ("0", "0"), plans
 
 
 @pytest.mark.parametrize("kind,it,ot,m,n,k", [
