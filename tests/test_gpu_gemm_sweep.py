@@ -115,3 +115,46 @@ def test_dequant_sweep(blas, capfd):
     assert not bad, bad
     cov = _covered(plans)
     assert all(cov.values()), cov
+
+
+def test_in_place_operand_sweep(blas, capfd):
+    """16-bit problems of the layouts other than (T, N) on the 128x128
+    kernel, drawn from a fixed seed: one pass, K slices and staged C (an
+    odd ldc), m a multiple of 8, n and the padding random, so that A and B
+    are read in place where their columns sit on 16 bytes and copied where
+    not. Bit-exact over the padded C with guard bands; the plan's direct_a /
+    direct_b must be what the alignment rule says, and the sweep must cover
+    both operands in place, a copy, K slices and a staged C."""
+    r = np.random.default_rng(20264)
+    bad, plans = [], []
+    for i in range(15):
+        in_t = _pick(r, [F16, BF16])
+        out_t = _pick(r, [F32, in_t])
+        ta, tb = _pick(r, [(0, 0), (0, 1), (1, 1)])
+        long_k = i % 3 == 2                     # few tiles, long K: K slices
+        m = 8 * int(r.integers(40, 80)) if long_k else 8 * int(r.integers(66, 140))
+        n = int(r.integers(300, 700)) if long_k else int(r.integers(520, 1100))
+        k = 8 * int(r.integers(300, 700)) if long_k else 8 * int(r.integers(8, 200))
+        pad = _pick(r, [0, 0, 8, 2])
+        cpad = _pick(r, [0, 8, 1]) if out_t != F32 else _pick(r, [0, 4, 1])
+        alpha, beta = _pick(r, [1.0, 2.5, -0.5]), _pick(r, [0.0, 1.0, -1.5])
+        res = []
+        got = logged_plans(capfd, lambda: res.append(
+            float_case(blas, in_t, out_t, ta, tb, m, n, k, alpha, beta, pad, cpad, seed=4000 + i,
+                       guard=True)))
+        plans += got
+        lda, ldb = (k if ta else m) + pad, (n if tb else k) + pad
+        ok = len(got) == 1 and res == [(0, 0)]
+        if ok and got[0]["kernel"] == "tn128" and pad != 2:
+            want_a = str(int(ta == 0 and lda % 8 == 0))
+            want_b = str(int(tb == 1 and n % 8 == 0 and ldb % 8 == 0))
+            ok = (got[0]["direct_a"], got[0]["direct_b"]) == (want_a, want_b)
+        if not ok:
+            bad.append((i, in_t, out_t, ta, tb, m, n, k, pad, cpad, res, got))
+    assert not bad, bad
+    cov = {"direct_a": any(p["direct_a"] == "1" for p in plans),
+           "direct_b": any(p["direct_b"] == "1" for p in plans),
+           "copy": any(p["copy_a"] == "1" or p["copy_b"] == "1" for p in plans),
+           "split": any(int(p["split"]) > 1 and p["direct_a"] + p["direct_b"] != "00" for p in plans),
+           "staged": any(p["staged"] == "1" and p["direct_a"] + p["direct_b"] != "00" for p in plans)}
+    assert all(cov.values()), (cov, plans)
