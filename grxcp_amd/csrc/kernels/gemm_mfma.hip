@@ -377,7 +377,12 @@ __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 // gemm_tn128's [k][m] layout of an M-contiguous A: 16-byte chunk XOR for
 // k-row k of a stage.
 __device__ __forceinline__ int an_swz(int k) { return 2 * ((k & 3) | ((k >> 2) & 4)); }
+// The same for int8 (k-rows of 128 bytes, 8 chunks): ((k >> 1) & 3) | bit 5
+// of k in bit 2.
+__device__ __forceinline__ int an_swz8(int k) { return ((k >> 1) & 3) | ((k >> 3) & 4); }
+template <int EB> __device__ __forceinline__ int nswz(int k) { return EB == 2 ? an_swz(k) : an_swz8(k); }
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -936,11 +941,15 @@ constexpr int kT128 = 128;
 // receiving the 4 k of its m), at the same k chunk as the B fragment of its
 // lanes, so every product is unchanged; over the 32 lanes of a read cycle
 // the swizzle puts the 8 rows' 16 chunks on distinct banks. BN: the same
-// for op(B) = B^T stored N-contiguous (transb = T).
+// for op(B) = B^T stored N-contiguous (transb = T). int8: 128 k-rows of 128
+// bytes per stage, chunks XOR-swizzled by an_swz8(k), each 16x16x64
+// fragment two ds_read_b64_tr_b8 (8 k-rows x 16 m, each lane receiving the 8
+// k of its m); over a read cycle's 32 lanes the 16 rows' chunks again fall
+// on distinct banks.
 template <class Op, MmaOut OUT, int NS, bool STREAM = true, bool AN = false, bool BN = false>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch_p) {
   static_assert(NS == 2 || NS == 4, "stages in the ring: 4 (one workgroup per CU) or 2 (two)");
-  static_assert((!AN && !BN) || Op::kElemBytes == 2, "M/N-contiguous operands: 16-bit inputs only");
+  static_assert((!AN && !BN) || Op::kElemBytes <= 2, "M/N-contiguous operands: 16-bit or int8 inputs");
   constexpr uint32_t kStage = kT128 * kChunks * 16;       // 16 KB per operand and stage
   const KParams p = batch_view(batch_p);
   // [A | B][stage][row * 8 + physical chunk], 16 bytes per entry.
@@ -962,7 +971,10 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
   const int rows_a = min(kT128, p.m - row0);
   const int rows_b = min(kT128, p.n - col0);
   constexpr uint32_t kOff = 0x80000000u;
-  constexpr int kRowsAN = kFastKBytes / 2;                // k-rows of an AN stage (64)
+  constexpr int EB = Op::kElemBytes;
+  constexpr int kRowsAN = kFastKBytes / EB;               // k-rows of an AN stage (64 or 128)
+  constexpr int kRowChunks = kT128 * EB / 16;             // 16-byte chunks of a k-row (16 or 8)
+  constexpr int kRowsDma = 64 / kRowChunks;               // k-rows per 1 KB DMA block (4 or 8)
   auto rsrc_words = [&](const uint8_t* base, int bytes) {
     const uint64_t a = (uint64_t)(uintptr_t)base;
     i32x4 r;
@@ -975,9 +987,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
   // AN: from the tile's first m; every k-row of A, to the end of the matrix
   // (m past the matrix within a row reads the next row's values, which only
   // reach rows of C that are never stored). BN likewise from the first n.
-  const i32x4 rsa = AN ? rsrc_words(p.a + (int64_t)row0 * 2, (p.k - 1) * lda_b + (p.m - row0) * 2)
+  const i32x4 rsa = AN ? rsrc_words(p.a + (int64_t)row0 * EB, (p.k - 1) * lda_b + (p.m - row0) * EB)
                        : rsrc_words(p.a + (int64_t)row0 * lda_b, (rows_a - 1) * lda_b + kbytes);
-  const i32x4 rsb = BN ? rsrc_words(p.b + (int64_t)col0 * 2, (p.k - 1) * ldb_b + (p.n - col0) * 2)
+  const i32x4 rsb = BN ? rsrc_words(p.b + (int64_t)col0 * EB, (p.k - 1) * ldb_b + (p.n - col0) * EB)
                        : rsrc_words(p.b + (int64_t)col0 * ldb_b, (rows_b - 1) * ldb_b + kbytes);
   // DMA instruction d (0..7) of a stage: operand d / 4, the 1 KB block of
   // rows 8*(4*(d%4) + wave) .. +7, lane L landing in row +L/8 at physical
@@ -989,11 +1001,10 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     const int blk = 4 * i + wave;
     const int row = 8 * blk + lr;
     const int c = pc ^ lr ^ (blk & 7);
-    base_a[i] = AN ? (uint32_t)((4 * blk + (lane >> 4)) * lda_b +
-                                16 * ((lane & 15) ^ an_swz(4 * blk + (lane >> 4))))
+    const int nrow = kRowsDma * blk + lane / kRowChunks;  // AN / BN: k-row of the stage
+    base_a[i] = AN ? (uint32_t)(nrow * lda_b + 16 * ((lane % kRowChunks) ^ nswz<EB>(nrow)))
                    : (uint32_t)(row * lda_b + 16 * c);
-    base_b[i] = BN ? (uint32_t)((4 * blk + (lane >> 4)) * ldb_b +
-                                16 * ((lane & 15) ^ an_swz(4 * blk + (lane >> 4))))
+    base_b[i] = BN ? (uint32_t)(nrow * ldb_b + 16 * ((lane % kRowChunks) ^ nswz<EB>(nrow)))
                    : (uint32_t)(row * ldb_b + 16 * c);
   }
   auto dma = [&](int kt, int st, int d) __attribute__((always_inline)) {
@@ -1005,8 +1016,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     // One wait state between the M0 write and the DMA that reads it (the
     // hazard pass does not look inside inline assembly).
     if ((d < 4 && AN) || (d >= 4 && BN)) {
-      // 4 k-rows of 256 bytes: lane L -> row 4*blk + L/16, physical chunk L%16
-      const int krow = kt * kRowsAN + 4 * blk + (lane >> 4);
+      // 4 k-rows of 256 bytes (int8: 8 of 128): lane L -> k-row
+      // kRowsDma*blk + L/kRowChunks, physical chunk L%kRowChunks
+      const int krow = kt * kRowsAN + kRowsDma * blk + lane / kRowChunks;
       const uint32_t ld = (uint32_t)(d < 4 ? lda_b : ldb_b);
       const uint32_t v = krow < p.k ? (d < 4 ? base_a[i] : base_b[i]) + (uint32_t)(kt * kRowsAN) * ld : kOff;
       const uint32_t l = (uint32_t)(uintptr_t)(lds_ptr_t)&lds[d < 4 ? 0 : 1][st][blk * 64];
@@ -1056,7 +1068,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
     }
   // AN / BN: per tile and k-step, the two transposing reads' addresses
   // (k-rows 8c .. 8c+3 and 8c+4 .. 8c+7 of chunk c = 4*ks + kq, m (or n) =
-  // 16t + 4*(j&3) for lane j of its 16-lane group).
+  // 16t + 4*(j&3) for lane j of its 16-lane group; int8: k-rows 16c .. +7
+  // and 16c+8 .. +15, m = 16t + 8*(j&1)).
   uint32_t ad_an[AN ? 4 : 1][2][2], ad_bn[BN ? 4 : 1][2][2];
   auto tr_addrs = [&](uint32_t (*ad)[2][2], int w, uint32_t base) __attribute__((always_inline)) {
     const int j = lane & 15;
@@ -1066,10 +1079,17 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int krow = 8 * (4 * ks + kq) + 4 * h + (j >> 2);
-          const int m = w * 64 + 16 * t + 4 * (j & 3);
-          ad[t][ks][h] = base + 256u * (uint32_t)krow + 16u * (uint32_t)((m >> 3) ^ an_swz(krow)) +
-                         2u * (uint32_t)(m & 7);
+          if constexpr (EB == 2) {
+            const int krow = 8 * (4 * ks + kq) + 4 * h + (j >> 2);
+            const int m = w * 64 + 16 * t + 4 * (j & 3);
+            ad[t][ks][h] = base + 256u * (uint32_t)krow + 16u * (uint32_t)((m >> 3) ^ an_swz(krow)) +
+                           2u * (uint32_t)(m & 7);
+          } else {
+            const int krow = 16 * (4 * ks + kq) + 8 * h + (j >> 1);
+            const int m = w * 64 + 16 * t + 8 * (j & 1);
+            ad[t][ks][h] = base + 128u * (uint32_t)krow + 16u * (uint32_t)((m >> 4) ^ an_swz8(krow)) +
+                           (uint32_t)(m & 15);
+          }
         }
   };
   if constexpr (AN) tr_addrs(ad_an, wm, lds0);
@@ -1077,9 +1097,15 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void gemm_tn128(KParams batch
   typedef __attribute__((address_space(3))) s16x4* lds_s16x4_t;
   auto frag_tr = [&](const uint32_t (*ad)[2][2], int t, int rks, uint32_t off)
       __attribute__((always_inline)) -> i32x4 {
-    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad[t][rks][0] + off));
-    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad[t][rks][1] + off));
-    const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+    u32x2 w0, w1;
+    if constexpr (EB == 2) {
+      w0 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad[t][rks][0] + off)));
+      w1 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(uintptr_t)(ad[t][rks][1] + off)));
+    } else {
+      typedef __attribute__((address_space(3))) i32x2* lds_i32x2_t;
+      w0 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t)(uintptr_t)(ad[t][rks][0] + off)));
+      w1 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t)(uintptr_t)(ad[t][rks][1] + off)));
+    }
     return i32x4{(int)w0.x, (int)w0.y, (int)w1.x, (int)w1.y};
   };
   i32x4 fa[2][4], fb[2][4];
@@ -1716,15 +1742,16 @@ bool c_ready(const GemmDesc& d) {
 // every chunk holding valid values is read whole; DMA offsets within the
 // 2^31 bytes a buffer offset reaches below the zero-fill offset (the last
 // k-row, plus a 128-row stage of slack).
-inline bool direct_ok(int rows, const void* x, int64_t ld, int64_t stride, int k) {
-  return rows % 8 == 0 && (uintptr_t)x % 16 == 0 && (ld * 2) % 16 == 0 && (stride * 2) % 16 == 0 &&
-         ((int64_t)k + kT128) * ld * 2 + 4096 < (1ll << 31);
+inline bool direct_ok(int eb, int rows, const void* x, int64_t ld, int64_t stride, int k) {
+  return (rows * eb) % 16 == 0 && (uintptr_t)x % 16 == 0 && (ld * eb) % 16 == 0 && (stride * eb) % 16 == 0 &&
+         ((int64_t)k + kT128) * ld * eb + 4096 < (1ll << 31);
 }
 
 template <class Op>
 Plan direct_operands(const GemmDesc& d, Plan t) {
-  if (Op::kElemBytes != 2 || !t.tn || !t.tn128 || t.kp != d.k) return t;
-  if (t.copy_a && !d.ta && direct_ok(d.m, d.a, d.lda, d.stride_a, d.k)) {
+  constexpr int EB = Op::kElemBytes;
+  if (EB > 2 || !t.tn || !t.tn128 || t.kp != d.k) return t;
+  if (t.copy_a && !d.ta && direct_ok(EB, d.m, d.a, d.lda, d.stride_a, d.k)) {
     t.copy_a = false;
     t.a_direct = true;
     t.batch_a = 0;
@@ -1734,7 +1761,7 @@ Plan direct_operands(const GemmDesc& d, Plan t) {
     t.e.lda = d.lda;
     t.e.stride_a = d.stride_a;
   }
-  if (t.copy_b && d.tb && direct_ok(d.n, d.b, d.ldb, d.stride_b, d.k)) {
+  if (t.copy_b && d.tb && direct_ok(EB, d.n, d.b, d.ldb, d.stride_b, d.k)) {
     t.copy_b = false;
     t.b_direct = true;
     t.batch_b = 0;
@@ -1882,7 +1909,7 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
         q.tiles_n = (g->n + kT128 - 1) / kT128;
         const dim3 grid(q.tiles_m * q.tiles_n, t.split);
         const int v = (t.tn128_stages == 2 ? 4 : 0) + (t.a_direct ? 1 : 0) + (t.b_direct ? 2 : 0);
-        if constexpr (Op::kElemBytes == 2) {      // operands read in place: 16-bit only
+        if constexpr (Op::kElemBytes <= 2) {      // operands read in place: 16-bit and int8
           switch (v) {
             case 1: hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false, true, false>), grid, dim3(256), 0, s, q); break;
             case 2: hipLaunchKernelGGL((gemm_tn128<Op, RAW, 4, false, false, true>), grid, dim3(256), 0, s, q); break;
@@ -1914,7 +1941,7 @@ hipError_t run(const GemmDesc& d, hipStream_t s) {
     p.tiles_n = (g->n + kT128 - 1) / kT128;
     if constexpr (Op::kM16)   // the plan takes this path for 16-bit and int8 inputs only
     {
-      if constexpr (Op::kElemBytes == 2) {
+      if constexpr (Op::kElemBytes <= 2) {
         if (t.a_direct || t.b_direct) {
           const dim3 grid(p.tiles_m * p.tiles_n, g->batch);
           const int v = (t.tn128_stages == 2 ? 4 : 0) + (t.a_direct ? 1 : 0) + (t.b_direct ? 2 : 0);

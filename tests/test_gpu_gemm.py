@@ -310,6 +310,35 @@ def test_direct_operands_exact(blas, capfd, it, ot, ta, tb, m, n, k, pad, alpha,
     assert p["copy_a"] == str(1 - ta - int(direct[0])) and p["copy_b"] == str(tb - int(direct[1])), plans
 
 
+@pytest.mark.parametrize("kind,ta,tb,m,n,k,direct,split", [
+    ("i8", 0, 0, 1024, 1040, 400, "10", False),
+    ("i8", 1, 1, 1040, 1024, 400, "01", False),
+    ("dq", 0, 1, 1024, 1024, 384, "11", False),
+    ("i8", 0, 1, 2176, 2176, 256, "11", False),    # 289 tiles: the two-stage ring
+    ("i8", 0, 0, 512, 256, 16384, "10", True),     # K slices
+    ("i8", 0, 0, 1032, 1040, 400, "00", False),    # m % 16 != 0: behind the copy
+])
+def test_direct_operands_int8_exact(blas, capfd, kind, ta, tb, m, n, k, direct, split):
+    """int8 problems on the 128x128 kernel read an M-contiguous A and an
+    N-contiguous B in place (128 k-rows of 128 bytes per stage, fragments
+    through ds_read_b64_tr_b8) where m (n) is a multiple of 16: int32 C and
+    the dequantised bf16 C bit-exact with guard bands."""
+    res = []
+    if kind == "i8":
+        call = lambda: res.append(int8_case(blas, ta, tb, m, n, k, 2.0, 1.0, 0, fill="rand",  # noqa: E731
+                                            seed=k + m, cpad=0, guard=True))
+        ok = 0
+    else:
+        call = lambda: res.append(dequant_case(blas, ta, tb, m, n, k, 0, 0, seed=k, guard=True))  # noqa: E731
+        ok = (0, 0)
+    plans = logged_plans(capfd, call)
+    assert res == [ok]
+    p = plans[0]
+    assert len(plans) == 1 and p["kernel"] == "tn128" and (int(p["split"]) > 1) == split, plans
+    assert p["direct_a"] + p["direct_b"] == direct, plans
+    assert p["copy_a"] == str(1 - ta - int(direct[0])) and p["copy_b"] == str(tb - int(direct[1])), plans
+
+
 @pytest.mark.parametrize("it,ot,ta,tb,m,n,k,cpad,split,staged,direct", [
     (BF16, F32, 0, 0, 512, 256, 4096, 0, True, "0", "10"),     # K slices
     (F16, F16, 1, 1, 512, 264, 4096, 0, True, "0", "01"),
