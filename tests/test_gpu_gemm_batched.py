@@ -170,8 +170,8 @@ def test_batched_runs_the_128_tile_kernel(blas, capfd):
 
 
 def test_batched_direct_operands(blas, capfd):
-    """16-bit batches on one pass of the 128x128 kernel read each batch's
-    M-contiguous A and N-contiguous B where they lie: strides packed,
+    """16-bit and int8 batches on one pass of the 128x128 kernel read each
+    batch's M-contiguous A and N-contiguous B where they lie: strides packed,
     broadcast (0) and negative, both rings, every batch bit-exact, C gaps
     untouched, no copy."""
     from test_gpu_gemm import logged_plans
@@ -179,12 +179,15 @@ def test_batched_direct_operands(blas, capfd):
              (F16, F32, 0, 0, 512, 512, 128, 32, "zero", "packed", "packed", "2"),
              (F16, F16, 0, 0, 256, 264, 512, 5, "packed", "zero", "gap", "4"),
              (BF16, F32, 0, 1, 256, 256, 512, 4, "packed", "neg", "gap", "4"),
-             (F16, F16, 1, 1, 264, 256, 512, 3, "zero", "zero", "packed", "4")]
+             (F16, F16, 1, 1, 264, 256, 512, 3, "zero", "zero", "packed", "4"),
+             (I8, I32, 0, 1, 256, 256, 512, 3, "neg", "packed", "gap", "4"),
+             (I8, I32, 0, 0, 512, 512, 128, 32, "packed", "zero", "packed", "2")]
     bad = []
     for it, ot, ta, tb, m, n, k, batch, am, bm, cm, ring in cases:
         res = []
+        alpha, beta = (2.0, -1.0) if it == I8 else (1.5, -0.5)   # int32 C: integral alpha, beta
         plans = logged_plans(capfd, lambda: res.append(batched_case(  # noqa: B023
-            blas, it, ot, ta, tb, m, n, k, 1.5, -0.5, batch, am, bm, cm, seed=batch)))
+            blas, it, ot, ta, tb, m, n, k, alpha, beta, batch, am, bm, cm, seed=batch)))
         if res != [0] or len(plans) != 1 or plans[0]["kernel"] != "tn128" or plans[0]["ring"] != ring \
                 or plans[0]["direct_a"] != str(1 - ta) or plans[0]["direct_b"] != str(tb) \
                 or plans[0]["copy_a"] != "0" or plans[0]["copy_b"] != "0":
